@@ -1,0 +1,391 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matmul hot path (libdeepinfer_hip) on one GPU.
+
+Headline (the JSON `value`): config 2 of BASELINE.json, one decode MoE step for one token
+(8-bit g64, 256 experts top-8, hidden 2048, intermediate 512, shared expert with a
+sigmoid gate) as achieved HBM GB/s of its algorithmic bytes. The other configs are
+measured in the same run and reported under "secondary". Weights and activations are
+seeded synthetic data created on the GPU; every timed step reads weights that are not
+resident in the 256 MB Infinity Cache (rotating copies whose working set between reuses
+exceeds 512 MB). Timed loops are captured in HIP graphs and replayed; per-stage HIP events
+inside the graph (on the stream the kernels run on) give each kernel's average duration
+over the timed region.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|qmv|prefill|
+                 prefill5|dense|lm_head] [--cpu-seconds S] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "infer.net_amd"))
+
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+H, E, I = 2048, 256, 512
+
+
+def metric_name():
+    try:
+        with open(os.path.join(ROOT, "BASELINE.json")) as f:
+            return json.load(f)["metric"]
+    except Exception:
+        return "decode qmv HBM GB/s (% peak); prefill MoE qmm TFLOP/s (% MFMA peak); tok/s"
+
+
+def qbytes(experts, rows, cols, bits):
+    """Algorithmic bytes of a packed matrix: codes + bf16 scale + bf16 bias per 64."""
+    return experts * rows * (cols * bits // 8 + (cols // 64) * 4)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self, args):
+        import torch
+        import deepinfer_hip as dh
+        self.torch, self.dh, self.args = torch, dh, args
+        torch.cuda.init()
+        self.dev = dh.QuantizedHip()
+        self.gen = torch.Generator(device="cuda")
+        self.gen.manual_seed(0)
+        self.keep = []
+
+    # ---------------------------------------------------------------- synthetic data
+    def matrix(self, experts, rows, cols, bits, scale=(5e-4, 2e-3)):
+        torch, dh = self.torch, self.dh
+        m = self.dev.allocate(experts, rows, cols, bits)
+        n_bytes = experts * rows * cols * bits // 8
+        step = 1 << 28
+        for off in range(0, n_bytes, step):
+            n = min(step, n_bytes - off)
+            codes = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=self.gen)
+            m.upload_from(0, codes, off)
+            del codes
+        ng = experts * rows * (cols // 64)
+        s = torch.empty(ng, device="cuda").uniform_(scale[0], scale[1], generator=self.gen).to(torch.bfloat16)
+        b = (-(1 << (bits - 1)) * s.float() + 1e-4 * torch.randn(ng, device="cuda", generator=self.gen)).to(torch.bfloat16)
+        m.upload_from(1, s)
+        m.upload_from(2, b)
+        return m
+
+    def bf16(self, *shape):
+        return self.torch.randn(*shape, device="cuda", generator=self.gen).to(self.torch.bfloat16)
+
+    def moe_layer(self, bits, with_router=True):
+        dh = self.dh
+        mats = dict(
+            router=self.matrix(1, E, H, 8, scale=(1.25e-4, 5e-4)) if with_router else None,
+            gate=self.matrix(E, I, H, bits), up=self.matrix(E, I, H, bits), down=self.matrix(E, H, I, bits),
+            shared_gate=self.matrix(1, I, H, bits), shared_up=self.matrix(1, I, H, bits),
+            shared_down=self.matrix(1, H, I, bits), shared_route=self.matrix(1, 1, H, 8))
+        self.keep.append(mats)
+        return mats, dh.make_layer(mats["router"], mats["gate"], mats["up"], mats["down"], mats["shared_gate"],
+                                   mats["shared_up"], mats["shared_down"], mats["shared_route"])
+
+    # ---------------------------------------------------------------- timing helper
+    def timed_graph(self, step_fn, steps, warmup):
+        """Runs `warmup` eager steps, captures `steps` steps into one graph with profiling
+        events, replays it once untimed, then times one replay. Returns (ms per step,
+        {stage: (ms total, launches)} of the timed replay)."""
+        torch, dh = self.torch, self.dh
+        # at least one eager step: scratch buffers must exist before capture
+        for i in range(max(1, warmup)):
+            step_fn(i)
+        torch.cuda.synchronize()
+        dh.set_profiling(self.dev, True)
+        g = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(steps):
+                    step_fn(i)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        prof = dh.profile_read(self.dev)
+        dh.set_profiling(self.dev, False)
+        del g
+        return (t1 - t0) * 1e3 / steps, prof
+
+    # ---------------------------------------------------------------- workloads
+    def decode(self, steps, warmup, layers=24):
+        """Config 2: decode MoE step, 8-bit, rotating `layers` layer copies (each ~855 MB)."""
+        torch, dh = self.torch, self.dh
+        log(f"[decode] building {layers} MoE layers (8-bit)")
+        built = [self.moe_layer(8) for _ in range(layers)]
+        xs = self.bf16(64, H)
+        res = self.bf16(H)
+
+        def step(i):
+            dh.moe_decode(self.dev, built[i % layers][1], xs[i % 64], res)
+
+        ms, prof = self.timed_graph(step, steps, warmup)
+        w_bytes = 9 * (2 * qbytes(1, I, H, 8) + qbytes(1, H, I, 8)) + qbytes(1, E, H, 8) + qbytes(1, 1, H, 8)
+        step_bytes = w_bytes + H * 2 + 2 * H * 2   # + x read, residual read/write
+        stage_bytes = {
+            "decode_router_shared": qbytes(1, E, H, 8) + qbytes(1, 1, H, 8) + 2 * qbytes(1, I, H, 8) + H * 2,
+            "decode_experts_gate_up": 16 * qbytes(1, I, H, 8) + qbytes(1, H, I, 8) + H * 2,
+            "decode_down_merge": 8 * qbytes(1, H, I, 8) + 2 * H * 2,
+        }
+        stages = {}
+        for name, (tot, cnt) in prof.items():
+            avg = tot / max(cnt, 1)
+            stages[name] = {"avg_us": avg * 1e3, "bytes": stage_bytes.get(name),
+                            "GB_s": stage_bytes.get(name, 0) / (avg * 1e-3) / 1e9 if avg > 0 else None}
+        self.free(built)
+        return {"ms_per_step": ms, "bytes_per_step": step_bytes, "GB_s": step_bytes / (ms * 1e-3) / 1e9,
+                "stages": stages}
+
+    def qmv(self, steps, warmup, copies=64):
+        """Config 1: one 8-bit [4096 x 2048] GEMV, bf16 in/out, rotating 64 weight copies."""
+        torch, dh = self.torch, self.dh
+        log(f"[qmv] building {copies} copies of 4096x2048 8-bit")
+        ms_ = [self.matrix(1, 4096, 2048, 8) for _ in range(copies)]
+        x = self.bf16(2048)
+        y = torch.zeros(4096, dtype=torch.bfloat16, device="cuda")
+
+        def step(i):
+            dh.qmv(self.dev, ms_[i % copies], x, y, y_dtype=dh.BF16)
+
+        ms, prof = self.timed_graph(step, steps, warmup)
+        b = qbytes(1, 4096, 2048, 8) + 2048 * 2 + 4096 * 2
+        tot, cnt = prof.get("qmv", (0.0, 1))
+        kern = tot / max(cnt, 1)
+        for m in ms_:
+            m.dispose()
+        return {"ms_per_step": ms, "bytes": b, "GB_s": b / (ms * 1e-3) / 1e9, "kernel_avg_us": kern * 1e3,
+                "kernel_GB_s": b / (kern * 1e-3) / 1e9 if kern > 0 else None}
+
+    def zipf_logits(self, T, s=1.1):
+        torch = self.torch
+        p = torch.arange(1, E + 1, dtype=torch.float64, device="cuda") ** -s
+        p = p / p.sum()
+        perm = torch.randperm(E, device="cuda", generator=self.gen)
+        u = torch.rand((T, E), dtype=torch.float64, device="cuda", generator=self.gen).clamp_(1e-12, 1 - 1e-12)
+        gumbel = -torch.log(-torch.log(u))
+        return (torch.log(p)[perm][None, :] + gumbel).to(torch.bfloat16)
+
+    def prefill(self, steps, warmup, T=512, bits=8, routing="zipf", layers=2):
+        """Configs 3/4: grouped prefill MoE chunk over `layers` rotating layer copies."""
+        torch, dh = self.torch, self.dh
+        log(f"[prefill] T={T} bits={bits} routing={routing}: building {layers} layers")
+        built = [self.moe_layer(bits, with_router=False) for _ in range(layers)]
+        x = self.bf16(T, H)
+        logits = self.zipf_logits(T) if routing == "zipf" else self.bf16(T, E)
+        res = self.bf16(T, H)
+        ids = torch.zeros((T, 8), dtype=torch.int32, device="cuda")
+        dh.moe_prefill(self.dev, built[0][1], T, x, logits, res, trace=dh.make_trace(ids=ids))
+        torch.cuda.synchronize()
+        counts = torch.bincount(ids.reshape(-1).long(), minlength=E)
+        touched = int((counts > 0).sum().item())
+
+        def step(i):
+            dh.moe_prefill(self.dev, built[i % layers][1], T, x, logits, res)
+
+        ms, prof = self.timed_graph(step, steps, warmup)
+        expert_w = 2 * qbytes(1, I, H, bits) + qbytes(1, H, I, bits)
+        w_bytes = (touched + 1) * expert_w + qbytes(1, 1, H, 8)
+        act_bytes = T * H * 2 * 3 + T * E * 2          # x read, residual read+write, logits
+        flops_routed = 2.0 * T * 8 * (2 * I * H + H * I)
+        flops_shared = 2.0 * T * (2 * I * H + H * I)
+        flops = flops_routed + flops_shared
+        stages = {}
+        for name, (tot, cnt) in prof.items():
+            stages[name] = {"avg_us": tot / max(cnt, 1) * 1e3}
+        gu = prof.get("prefill_gate_up", (0, 1))
+        dn = prof.get("prefill_down", (0, 1))
+        gu_ms, dn_ms = gu[0] / max(gu[1], 1), dn[0] / max(dn[1], 1)
+        gu_bytes = (touched + 1) * 2 * qbytes(1, I, H, bits)
+        dn_bytes = (touched + 1) * qbytes(1, H, I, bits)
+        if gu_ms > 0:
+            stages["prefill_gate_up"].update(
+                bytes=gu_bytes, GB_s=gu_bytes / (gu_ms * 1e-3) / 1e9,
+                TFLOP_s=(2.0 / 3.0) * flops / (gu_ms * 1e-3) / 1e12)
+        if dn_ms > 0:
+            stages["prefill_down"].update(
+                bytes=dn_bytes, GB_s=dn_bytes / (dn_ms * 1e-3) / 1e9,
+                TFLOP_s=(1.0 / 3.0) * flops / (dn_ms * 1e-3) / 1e12)
+        self.free(built)
+        tf = flops / (ms * 1e-3) / 1e12
+        return {"tokens": T, "bits": bits, "routing": routing, "experts_touched": touched,
+                "max_routes_per_expert": int(counts.max().item()), "ms_per_step": ms,
+                "weight_bytes": w_bytes, "GB_s": (w_bytes + act_bytes) / (ms * 1e-3) / 1e9,
+                "GFLOP": flops / 1e9, "TFLOP_s": tf, "mfma_frac": tf / PEAK_BF16_TFLOPS,
+                "hbm_frac": (w_bytes + act_bytes) / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                "tok_s_per_layer": T / (ms * 1e-3), "stages": stages}
+
+    def dense(self, steps, warmup, T=4096):
+        """Config 5: dense 8-bit projections at a 4096-token chunk."""
+        torch, dh = self.torch, self.dh
+        shapes = {"q_gate": (8192, 2048), "k": (512, 2048), "v": (512, 2048), "o": (2048, 4096),
+                  "in_proj": (12288, 2048)}
+        out = {}
+        for name, (R, C) in shapes.items():
+            m = self.matrix(1, R, C, 8)
+            x = self.bf16(T, C)
+            y = torch.zeros((T, R), dtype=torch.bfloat16, device="cuda")
+
+            def step(i, m=m, x=x, y=y, T=T):
+                dh.dense(self.dev, m, T, x, y, y_dtype=dh.BF16)
+
+            ms, prof = self.timed_graph(step, max(2, steps // 4), min(warmup, 3))
+            tot, cnt = prof.get("dense_qmm", (0, 1))
+            kern = tot / max(cnt, 1)
+            flops = 2.0 * T * R * C
+            out[name] = {"rows": R, "cols": C, "ms": ms, "TFLOP_s": flops / (ms * 1e-3) / 1e12,
+                         "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         "kernel_avg_us": kern * 1e3}
+            m.dispose()
+            del x, y
+        tot_f = sum(2.0 * T * r * c for r, c in shapes.values())
+        tot_ms = sum(v["ms"] for v in out.values())
+        return {"tokens": T, "per_matrix": out, "TFLOP_s": tot_f / (tot_ms * 1e-3) / 1e12,
+                "mfma_frac": tot_f / (tot_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+
+    def lm_head(self, steps, warmup, copies=2):
+        """Config 5b: lm_head [248320 x 2048] 8-bit in 4 vocab slices, f32 logits, argmax."""
+        torch, dh = self.torch, self.dh
+        log(f"[lm_head] building {copies} copies of 4 x 62080 x 2048 8-bit")
+        sets = [[self.matrix(1, 62080, 2048, 8) for _ in range(4)] for _ in range(copies)]
+        x = self.bf16(2048)
+        logits = torch.zeros(248320, dtype=torch.float32, device="cuda")
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+        def step(i):
+            dh.lm_head(self.dev, sets[i % copies], x, logits, nxt)
+
+        ms, prof = self.timed_graph(step, max(2, steps // 4), min(warmup, 3))
+        b = qbytes(1, 248320, 2048, 8) + 2048 * 2 + 248320 * 4
+        tot, cnt = prof.get("lm_head_qmv", (0, 1))
+        kern = tot / max(cnt, 1)
+        for s in sets:
+            for m in s:
+                m.dispose()
+        return {"ms_per_step": ms, "bytes": b, "GB_s": b / (ms * 1e-3) / 1e9,
+                "qmv_kernel_avg_us": kern * 1e3,
+                "qmv_kernel_GB_s": (b - 248320 * 4) / (kern * 1e-3) / 1e9 if kern > 0 else None}
+
+    def free(self, built):
+        for mats, _ in built:
+            for m in mats.values():
+                if m is not None:
+                    m.dispose()
+        self.keep = [k for k in self.keep if all(k is not b[0] for b in built)]
+        self.torch.cuda.empty_cache()
+
+
+def cpu_baseline(seconds):
+    """The reference's CPU dequant-then-matmul path (oracle/oracle.c restatement of
+    MatVec.cs:40-55 + quantized.mm:384-397, composed per Qwen36Model.cs:218-262) timed for
+    config 2 on this host, single-threaded like the reference."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    rng = np.random.default_rng(0)
+    L = orc.MoeLayer(orc.random_matrix(rng, 1, E, H, 8, 1.25e-4, 5e-4), orc.random_matrix(rng, E, I, H, 8),
+                     orc.random_matrix(rng, E, I, H, 8), orc.random_matrix(rng, E, H, I, 8),
+                     orc.random_matrix(rng, 1, I, H, 8), orc.random_matrix(rng, 1, I, H, 8),
+                     orc.random_matrix(rng, 1, H, I, 8), orc.random_matrix(rng, 1, 1, H, 8))
+    xs = orc.round_bf16(rng.normal(size=(16, H)).astype(np.float32))
+    orc.cpu_moe_token(L, xs[0])
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        orc.cpu_moe_token(L, xs[n % 16], threads=1)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    b = 9 * (2 * qbytes(1, I, H, 8) + qbytes(1, H, I, 8)) + qbytes(1, E, H, 8) + qbytes(1, 1, H, 8) + 6 * H
+    return {"value": b / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} decode MoE steps (config 2, one 8-bit layer) in {n * dt:.1f} s, "
+                      f"{dt * 1e3:.1f} ms/step, oracle/oracle.c orc_cpu_moe_token",
+            "ms_per_step": dt * 1e3}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--workload", default="all")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs as a single process on one GPU.", file=sys.stderr)
+        sys.exit(2)
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+    b = Bench(args)
+    wl = args.workload
+    res = {}
+    if wl in ("all", "decode"):
+        res["decode"] = b.decode(steps, warmup)
+        log(f"[decode] {res['decode']['GB_s']:.0f} GB/s, {res['decode']['ms_per_step'] * 1e3:.2f} us/step")
+    if wl in ("all", "qmv"):
+        res["qmv"] = b.qmv(steps, warmup)
+        log(f"[qmv] {res['qmv']['GB_s']:.0f} GB/s")
+    if wl in ("all", "prefill"):
+        res["prefill"] = b.prefill(max(2, steps // 12), min(warmup, 3))
+        log(f"[prefill] {res['prefill']['TFLOP_s']:.1f} TFLOP/s, {res['prefill']['GB_s']:.0f} GB/s")
+    if wl in ("all", "prefill5"):
+        res["prefill5"] = b.prefill(max(2, steps // 24), min(warmup, 2), T=2048, bits=5, routing="uniform")
+        log(f"[prefill5] {res['prefill5']['TFLOP_s']:.1f} TFLOP/s, {res['prefill5']['GB_s']:.0f} GB/s")
+    if wl in ("all", "dense"):
+        res["dense"] = b.dense(steps, warmup)
+        log(f"[dense] {res['dense']['TFLOP_s']:.1f} TFLOP/s")
+    if wl in ("all", "lm_head"):
+        res["lm_head"] = b.lm_head(steps, warmup)
+        log(f"[lm_head] {res['lm_head']['GB_s']:.0f} GB/s")
+
+    if "decode" in res:
+        d = res["decode"]
+        head = {"metric": metric_name(), "value": d["GB_s"], "unit": "GB/s", "ms_per_step": d["ms_per_step"],
+                "dtype": "f32", "percent_of_peak": 100.0 * d["GB_s"] / PEAK_HBM_GBS,
+                "config": {"workload": "decode MoE step (BASELINE config 2): 1 token, 8-bit g64, 256 experts "
+                                       "top-8, hidden 2048, intermediate 512, shared expert + sigmoid gate, "
+                                       "router GEMV, weighted sum into a bf16 residual; 24 rotating layer copies",
+                           "bytes_per_step": d["bytes_per_step"], "layers_rotated": 24}}
+        dom = max(d["stages"].items(), key=lambda kv: kv[1]["avg_us"])
+        roof = {"kernel": dom[0], "bound": "hbm", "achieved": dom[1]["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": dom[1]["GB_s"] / PEAK_HBM_GBS if dom[1]["GB_s"] else None, "traffic": None,
+                "avg_us": dom[1]["avg_us"], "bytes_per_launch": dom[1]["bytes"]}
+    else:
+        k, v = next(iter(res.items()))
+        head = {"metric": metric_name(), "value": v.get("GB_s") or v.get("TFLOP_s"),
+                "unit": "GB/s" if "GB_s" in v else "TFLOP/s", "ms_per_step": v.get("ms_per_step", v.get("ms")),
+                "dtype": "bf16" if k in ("prefill", "prefill5", "dense") else "f32", "config": {"workload": k}}
+        roof = None
+    tok = None
+    if "decode" in res and "lm_head" in res:
+        per_token_ms = 40 * res["decode"]["ms_per_step"] + res["lm_head"]["ms_per_step"]
+        tok = {"decode_path_tok_s": 1e3 / per_token_ms,
+               "note": "kernel-sum of this path only (40 MoE layers + lm_head), not model throughput"}
+    cpu = None
+    if not args.no_cpu and wl in ("all", "decode"):
+        log(f"[cpu] timing the CPU baseline for ~{args.cpu_seconds:.0f} s")
+        cpu = cpu_baseline(args.cpu_seconds)
+    line = {"metric": head["metric"], "value": head["value"], "unit": head["unit"], "n_gpus": 1,
+            "steps": steps, "warmup": warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": head["dtype"], "data": "synthetic",
+            "config": head["config"], "roofline": roof, "cpu_baseline": cpu, "tok_s": tok,
+            "secondary": {k: v for k, v in res.items() if k != "decode"}}
+    if "decode" in res:
+        line["secondary"]["decode_stages"] = res["decode"]["stages"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,228 @@
+/*
+ * deepinfer_hip.h - C ABI of libdeepinfer_hip, the MI355X (gfx950) quantized-matmul
+ * library for Qwen3.6-35B-A3B MLX-affine group-64 weights (5-bit and 8-bit).
+ *
+ * Conventions shared by every entry point:
+ *   - Handles are opaque pointers. Functions returning a handle return NULL on failure.
+ *   - Functions returning int return 0 on success and -1 on failure.
+ *   - `error`/`capacity`: a caller buffer (the managed caller uses 2048 bytes) that
+ *     receives a NUL-terminated UTF-8 message on failure (bridge.mm:9-15).
+ *   - Every argument is validated before any GPU work is queued: an invalid call
+ *     launches nothing and leaves outputs untouched (QuantizedTests.cs:118-135, 210-227).
+ *   - Weight layout is the checkpoint's MLX affine layout, unchanged:
+ *       packed  uint32 [experts, rows, columns*bits/32], codes LSB-first (bit c*bits)
+ *       scales  bf16   [experts, rows, columns/64]
+ *       biases  bf16   [experts, rows, columns/64]
+ *     w = float(code)*scale + bias (quantized.mm:41-53).
+ *   - Entry points whose name does not start with dih_quant_ take DEVICE pointers and a
+ *     hipStream_t passed as void* (NULL = the context's own stream). They only enqueue
+ *     work; the caller synchronizes the stream. bf16 buffers are raw uint16 bit patterns.
+ *   - Entry points named dih_quant_* take HOST pointers and are synchronous, like the
+ *     reference's di_quant_* functions.
+ *   - A context is single-stream and has no internal locking: callers serialize calls on
+ *     one context (the reference serializes through Qwen36Model.cs:18, 47).
+ */
+#ifndef DEEPINFER_HIP_H
+#define DEEPINFER_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One independent GEMV job. Same field order and sizes as QuantJob (quantized.mm:24-30)
+ * and QuantNative.Job (QuantizedMetal.cs:250-258). */
+typedef struct dih_job {
+    void *matrix;
+    const float *input;
+    float *output;
+    const uint32_t *experts;
+    int32_t count, batched;
+} dih_job;
+
+/* ---- context ------------------------------------------------------------------- */
+
+/* Replaces di_quant_create (quantized.mm:287-292). Uses device 0 of the process's
+ * visible HIP devices and creates one non-blocking stream. */
+void *dih_quant_create(char *error, int capacity);
+/* Replaces di_quant_create_configured (quantized.mm:245-286). `resident` (0/1) and
+ * `refresh` (0..60000 ms) are validated like the reference; HIP device memory needs no
+ * residency set, so `resident` only switches dih_quant_residency_bytes reporting on. */
+void *dih_quant_create_configured(int resident, int refresh, char *error, int capacity);
+/* Replaces di_quant_destroy (quantized.mm:299). Frees every scratch buffer. */
+void dih_quant_destroy(void *context);
+/* Replaces di_quant_residency_bytes (quantized.mm:293-295): device bytes held by the
+ * weights of live matrices when created with resident=1, else 0. */
+uint64_t dih_quant_residency_bytes(void *context);
+/* Replaces di_quant_residency_prepare (quantized.mm:296-298). No work on HIP. */
+void dih_quant_residency_prepare(void *context);
+
+/* ---- matrices -------------------------------------------------------------------- */
+
+/* Replaces di_quant_matrix_create (quantized.mm:300-320). Checks 1<=experts<=256,
+ * rows>=1, columns a multiple of 64 (at most 8192), bits 5 or 8, group 64. */
+void *dih_quant_matrix_create(void *context, int experts, int rows, int columns, int bits,
+                              int group, char *error, int capacity);
+/* Replaces di_quant_matrix_buffer (quantized.mm:321-324). index 0 packed, 1 scales,
+ * 2 biases. Metal returns unified memory; here the pointer is a pinned HOST staging
+ * copy of that buffer. Asking for the pointer marks the buffer dirty and the next call
+ * that reads the matrix uploads it, so `write through the pointer, then multiply`
+ * (QuantizedMetal.cs:171-178) works unchanged. NULL on a bad index. */
+void *dih_quant_matrix_buffer(void *matrix, int index);
+/* Replaces di_quant_matrix_destroy (quantized.mm:325). */
+void dih_quant_matrix_destroy(void *matrix);
+
+/* New (HIP has no unified memory): copies `bytes` from `source` (host or device memory)
+ * into buffer
+ * `index` at byte `offset` of the device copy directly, without a staging copy. */
+int dih_quant_matrix_write(void *matrix, int index, size_t offset, const void *source,
+                           size_t bytes, char *error, int capacity);
+/* New: uploads a dirty staging buffer now and releases the host staging copy. */
+int dih_quant_matrix_commit(void *matrix, char *error, int capacity);
+/* New: device pointer of buffer `index` (0 packed, 1 scales, 2 biases) for callers
+ * that fill weights on the device; uploads a dirty staging copy first. */
+void *dih_quant_matrix_device(void *matrix, int index);
+/* New: shape query; any out pointer may be NULL. */
+int dih_quant_matrix_shape(void *matrix, int *experts, int *rows, int *columns, int *bits);
+
+/* ---- synchronous host-pointer compute (reference ABI) ---------------------------- */
+
+/* Replaces di_quant_batch (quantized.mm:326-352): 1..8 jobs with distinct matrices;
+ * y[slot*rows+row] = sum_c w(experts[slot],row,c) * x[(batched?slot*columns:0)+c].
+ * `ms` receives the GPU interval of the submission. */
+int dih_quant_batch(void *context, const dih_job *jobs, int count, double *ms, char *error,
+                    int capacity);
+/* Replaces di_quant_matvec (quantized.mm:353-356). */
+int dih_quant_matvec(void *context, void *matrix, const float *x, float *out,
+                     const uint32_t *experts, int count, int batched, double *ms, char *error,
+                     int capacity);
+/* Replaces di_quant_experts (quantized.mm:357-383): per slot, act = silu(gate.x)*(up.x),
+ * out[slot] = down[expert].act; sharedOut = shared.sharedInput. Three kernels, one
+ * submission. */
+int dih_quant_experts(void *context, void *gate, void *up, void *down, void *shared,
+                      const float *input, const float *sharedInput, const uint32_t *experts,
+                      int count, float *expertOutput, float *sharedOutput, double *ms,
+                      char *error, int capacity);
+/* Replaces di_quant_embedding (quantized.mm:384-397): dequantizes row `token` of a
+ * single-expert matrix into out[columns]. Returns -1 on bad arguments. */
+int dih_quant_embedding(void *matrix, int token, float *out);
+
+/* ---- device-resident hot path ------------------------------------------------------ */
+
+enum { DIH_F32 = 0, DIH_BF16 = 1 };
+
+/* Decode qmv (M=1 GEMV, quant_rows semantics quantized.mm:119-144 and g_gemv
+ * gpu_graph.mm:285-294). x is bf16 or f32 [count or 1][columns]; y is f32 or bf16
+ * [count][rows]. `experts` is a DEVICE array of `count` ids or NULL (expert 0,
+ * count must be 1); an id >= experts yields NaN outputs for its slot. */
+int dih_qmv(void *context, void *matrix, const void *x, int x_dtype, void *y, int y_dtype,
+            const uint32_t *experts, int count, int batched, void *stream, char *error,
+            int capacity);
+
+/* Fused gate/up + SwiGLU GEMV (expert_gate_up, quantized.mm:148-189):
+ * act[slot*rows+row] = silu(gate.x) * (up.x), f32 output. x is shared by all slots. */
+int dih_qmv_swiglu(void *context, void *gate, void *up, const void *x, int x_dtype,
+                   float *act, const uint32_t *experts, int count, void *stream, char *error,
+                   int capacity);
+
+/* Split lm_head + argmax (classifier GEMV gpu_graph.mm:446-448; argmax
+ * gpu_graph.mm:160-175). `slices` are single-expert 8- or 5-bit matrices with the same
+ * columns whose rows concatenate to the vocabulary; x is bf16 [columns]; logits f32
+ * [sum rows]; next (u32, device) = lowest index of the maximum, 0xffffffff when any
+ * logit is not finite. */
+int dih_lm_head(void *context, void *const *slices, int slice_count, const void *x,
+                float *logits, uint32_t *next, void *stream, char *error, int capacity);
+
+/* Argmax alone over n f32 device values (gpu_graph.mm:160-175). */
+int dih_argmax(void *context, const float *values, int n, uint32_t *next, void *stream,
+               char *error, int capacity);
+
+/* Router selection: per token top-8 of `experts` logits (f32 or bf16 [tokens][experts]),
+ * ties to the lowest id, probabilities = softmax over the eight chosen logits
+ * (Qwen36Model.cs:246-262, graph_top8 gpu_graph.mm:134-146). ids u32 [tokens][8],
+ * probs f32 [tokens][8]. `status` (device u32, may be NULL) is set to 1 when a logit
+ * is not finite (the reference throws, Qwen36Model.cs:252). experts <= 256. */
+int dih_top8(void *context, const void *logits, int logits_dtype, int tokens, int experts,
+             uint32_t *ids, float *probs, uint32_t *status, void *stream, char *error,
+             int capacity);
+
+/* Route grouping (prefill_build_groups, prefill_moe.mm:8-17, made deterministic):
+ * counts[e] = routes r = t*8+slot with ids[r]==e; routes[e*tokens + k] lists them in
+ * ascending order. Devices arrays: ids u32 [tokens*8], counts u32 [experts],
+ * routes u32 [experts*tokens]. */
+int dih_build_groups(void *context, const uint32_t *ids, int tokens, int experts,
+                     uint32_t *counts, uint32_t *routes, void *stream, char *error,
+                     int capacity);
+
+/* Dequantize one expert of a matrix to bf16 [rows][columns] with round-to-nearest-even
+ * (expanded_weights, prefill_bf16_expanded.mm:8-16). */
+int dih_dequant_bf16(void *context, void *matrix, int expert, uint16_t *out, void *stream,
+                     char *error, int capacity);
+
+/* Weights of one MoE layer (Qwen36Weights.cs:93-100). router and shared_route are
+ * 8-bit; gate/up [E, I, H], down [E, H, I], shared_gate/shared_up [1, Is, H],
+ * shared_down [1, H, Is], shared_route [1, 1, H]. router may be NULL when the caller
+ * supplies logits. */
+typedef struct dih_moe_layer {
+    void *router;
+    void *gate, *up, *down;
+    void *shared_gate, *shared_up, *shared_down;
+    void *shared_route;
+} dih_moe_layer;
+
+/* Optional device outputs for inspection; any field may be NULL. */
+typedef struct dih_moe_trace {
+    float *logits;    /* f32 [tokens][E] router logits (decode: computed; prefill: copied) */
+    uint32_t *ids;    /* u32 [tokens][8] */
+    float *probs;     /* f32 [tokens][8] */
+    float *expert_out;/* f32 [tokens*8 + tokens][H] per-route down outputs before weighting
+                         (decode: the 8 slots then the shared expert, like the outputs of
+                         di_quant_experts); shared expert rows follow the routed ones */
+    uint32_t *status; /* u32, set to 1 when a router logit is not finite (the reference
+                         throws, Qwen36Model.cs:252); the caller zeroes it */
+} dih_moe_trace;
+
+/* Decode MoE step for one token (g_router, gpu_graph.mm:307-320, host form
+ * Qwen36Model.cs:218-245): logits = router.x (or `logits` if non-NULL, f32 [E]),
+ * top-8, act = silu(gate.x)*(up.x) for the 8 experts and the shared expert,
+ * y = sigmoid(shared_route.x)*shared_down.sact + sum_slot p_slot*down[e_slot].act_slot
+ * (slot order 0..7), residual = bf16(residual + y). x, residual: bf16 [H]. */
+int dih_moe_decode(void *context, const dih_moe_layer *layer, const void *x,
+                   const float *logits, void *residual, const dih_moe_trace *trace,
+                   void *stream, char *error, int capacity);
+
+/* Prefill MoE chunk (gpu_prefill.mm:700-706 with packed_expert_gate_fused /
+ * packed_expert_down, prefill_expert_packed.mm, and prefill_merge gpu_prefill.mm:140-150):
+ * top-8 of logits (bf16 or f32 [T][E]) -> grouped per-expert route lists -> bf16 MFMA
+ * gate/up + SwiGLU over gathered tokens -> bf16 MFMA down -> weighted sum with the
+ * sigmoid-gated shared expert -> residual = bf16(residual + y). x, residual bf16 [T][H].
+ * Scratch lives in the context and grows on demand (hipMalloc only when a larger chunk
+ * than any before is seen). */
+int dih_moe_prefill(void *context, const dih_moe_layer *layer, int tokens, const void *x,
+                    const void *logits, int logits_dtype, void *residual,
+                    const dih_moe_trace *trace, void *stream, char *error, int capacity);
+
+/* Dense batched projection through the same MFMA qmm (p_gemv dense path,
+ * gpu_prefill.mm:603-614, prefill_bf16.mm:7-53): Y[t][r] = sum_c w(0,r,c)*X[t][c],
+ * bf16 operands, f32 accumulation. x bf16 [T][C]; y f32 or bf16 [T][R]. */
+int dih_dense(void *context, void *matrix, int tokens, const void *x, void *y, int y_dtype,
+              void *stream, char *error, int capacity);
+
+/* Per-stage GPU timing (the reference's DEEPINFER_METAL_GPU_PROFILE per-dispatch
+ * timestamps, gpu_graph.mm:329-338, as a runtime switch instead of getenv). While enabled,
+ * every device-resident call records HIP events on its own stream between its kernels.
+ * dih_set_profiling clears the records (and synchronizes the device if any were taken);
+ * dih_profile_read waits for the last event and writes, per distinct stage name, the summed
+ * milliseconds and the number of recorded launches. Returns the number of stages. */
+int dih_set_profiling(void *context, int enabled);
+int dih_profile_read(void *context, double *total_ms, int *counts, const char **names,
+                     int capacity);
+
+/* Library build string (kernels' target and version). */
+const char *dih_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,894 @@
+// C ABI of libdeepinfer_hip (declared in include/deepinfer_hip.h). Every entry point
+// validates all arguments before queuing GPU work (QuantizedTests.cs:118-135, 210-227).
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+
+#include "dih_internal.h"
+
+namespace dih {
+
+void set_error(char *error, int capacity, const std::string &message) {
+    if (error && capacity > 0) {
+        size_t n = std::min(message.size(), (size_t)capacity - 1);
+        memcpy(error, message.data(), n);
+        error[n] = 0;
+    }
+}
+
+bool hip_ok(hipError_t e, char *error, int capacity, const char *what) {
+    if (e == hipSuccess) return true;
+    set_error(error, capacity, std::string(what) + ": " + hipGetErrorString(e));
+    return false;
+}
+
+void *scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity) {
+    Scratch &s = c->ws[id];
+    if (bytes == 0) bytes = 4;
+    if (s.bytes >= bytes) return s.ptr;
+    if (s.ptr) {
+        // Growth is rare; make sure no queued kernel still uses the old block.
+        if (!hip_ok(hipDeviceSynchronize(), error, capacity, "scratch sync")) return nullptr;
+        (void)hipFree(s.ptr);
+        s.ptr = nullptr;
+        s.bytes = 0;
+    }
+    size_t rounded = (bytes + 255) & ~(size_t)255;
+    if (!hip_ok(hipMalloc(&s.ptr, rounded), error, capacity, "scratch allocation")) return nullptr;
+    if (!hip_ok(hipMemset(s.ptr, 0, rounded), error, capacity, "scratch clear")) return nullptr;
+    s.bytes = rounded;
+    return s.ptr;
+}
+
+bool sync_matrix(Matrix *m, char *error, int capacity) {
+    for (int i = 0; i < 3; i++) {
+        if (m->dirty[i] && m->host[i]) {
+            if (!hip_ok(hipMemcpy(m->dev[i], m->host[i], m->bytes[i], hipMemcpyHostToDevice), error,
+                        capacity, "weight upload"))
+                return false;
+            m->dirty[i] = false;
+        }
+    }
+    return true;
+}
+
+static int prof_event(Context *c, hipStream_t s) {
+    if (c->prof_used == (int)c->prof_pool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return -1;
+        c->prof_pool.push_back(e);
+    }
+    const int i = c->prof_used++;
+    // Inside stream capture the event becomes an external record node of the graph, so
+    // every replay re-records it and reading after a replay times that replay's stages.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    (void)hipStreamIsCapturing(s, &cap);
+    hipError_t e = cap == hipStreamCaptureStatusActive
+                       ? hipEventRecordWithFlags(c->prof_pool[i], s, hipEventRecordExternal)
+                       : hipEventRecord(c->prof_pool[i], s);
+    if (e != hipSuccess) return -1;
+    return i;
+}
+
+void prof_begin(Context *c, hipStream_t s) {
+    if (!c->profiling) return;
+    c->prof_last = prof_event(c, s);
+}
+
+void prof_mark(Context *c, hipStream_t s, const char *name) {
+    if (!c->profiling || c->prof_last < 0) return;
+    const int e = prof_event(c, s);
+    if (e < 0) return;
+    c->prof_recs.push_back({c->prof_last, e, name});
+    c->prof_last = e;
+}
+
+static Context *as_ctx(void *p) {
+    auto *c = static_cast<Context *>(p);
+    return c && c->magic == 0x44494358u ? c : nullptr;
+}
+static Matrix *as_mat(void *p) {
+    auto *m = static_cast<Matrix *>(p);
+    return m && m->magic == 0x44494d58u ? m : nullptr;
+}
+static hipStream_t pick(Context *c, void *stream) {
+    return stream ? static_cast<hipStream_t>(stream) : c->stream;
+}
+
+static bool stage(Matrix *m, size_t in_floats, size_t out_floats, char *error, int capacity) {
+    if (m->stage_in_bytes < in_floats * 4) {
+        if (m->stage_in) (void)hipFree(m->stage_in);
+        m->stage_in = nullptr;
+        m->stage_in_bytes = 0;
+        if (!hip_ok(hipMalloc(&m->stage_in, in_floats * 4), error, capacity, "staging allocation")) return false;
+        m->stage_in_bytes = in_floats * 4;
+    }
+    if (m->stage_out_bytes < out_floats * 4) {
+        if (m->stage_out) (void)hipFree(m->stage_out);
+        m->stage_out = nullptr;
+        m->stage_out_bytes = 0;
+        if (!hip_ok(hipMalloc(&m->stage_out, out_floats * 4), error, capacity, "staging allocation")) return false;
+        m->stage_out_bytes = out_floats * 4;
+    }
+    return true;
+}
+
+static QmvSeg seg_of(const Matrix *m) {
+    QmvSeg s;
+    s.p0 = m->packed(); s.s0 = m->scales(); s.b0 = m->biases();
+    s.rows = m->rows; s.columns = m->columns; s.experts = m->experts;
+    return s;
+}
+
+static int cpl_of(int columns) { return (columns / 32 + 63) / 64; }
+
+}  // namespace dih
+
+using namespace dih;
+
+extern "C" {
+
+__attribute__((visibility("default"))) const char *dih_version(void) {
+    return "deepinfer_hip 0.1 gfx950 (wave64, bf16 MFMA 32x32x16)";
+}
+
+__attribute__((visibility("default"))) void *dih_quant_create_configured(int resident, int refresh,
+                                                                         char *error, int capacity) {
+    if ((resident != 0 && resident != 1) || refresh < 0 || refresh > 60000) {
+        set_error(error, capacity, "Invalid residency configuration");
+        return nullptr;
+    }
+    int count = 0;
+    if (!hip_ok(hipGetDeviceCount(&count), error, capacity, "device query")) return nullptr;
+    if (count < 1) {
+        set_error(error, capacity, "No HIP device");
+        return nullptr;
+    }
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), error, capacity, "device query")) return nullptr;
+    hipDeviceProp_t prop;
+    if (!hip_ok(hipGetDeviceProperties(&prop, dev), error, capacity, "device query")) return nullptr;
+    if (prop.warpSize != 64 || strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_error(error, capacity, std::string("Quantized kernels require gfx950 (wave64); found ") + prop.gcnArchName);
+        return nullptr;
+    }
+    auto *c = new (std::nothrow) Context();
+    if (!c) {
+        set_error(error, capacity, "Out of host memory");
+        return nullptr;
+    }
+    c->device = dev;
+    c->resident = resident == 1;
+    if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), error, capacity, "stream") ||
+        !hip_ok(hipEventCreate(&c->start), error, capacity, "event") ||
+        !hip_ok(hipEventCreate(&c->stop), error, capacity, "event")) {
+        delete c;
+        return nullptr;
+    }
+    return c;
+}
+
+__attribute__((visibility("default"))) void *dih_quant_create(char *error, int capacity) {
+    return dih_quant_create_configured(0, 1000, error, capacity);
+}
+
+__attribute__((visibility("default"))) void dih_quant_destroy(void *p) {
+    Context *c = as_ctx(p);
+    if (!c) return;
+    (void)hipStreamSynchronize(c->stream);
+    for (auto &s : c->ws)
+        if (s.ptr) (void)hipFree(s.ptr);
+    for (auto &e : c->prof_pool) (void)hipEventDestroy(e);
+    (void)hipEventDestroy(c->start);
+    (void)hipEventDestroy(c->stop);
+    (void)hipStreamDestroy(c->stream);
+    c->magic = 0;
+    delete c;
+}
+
+__attribute__((visibility("default"))) uint64_t dih_quant_residency_bytes(void *p) {
+    Context *c = as_ctx(p);
+    return c && c->resident ? c->weight_bytes : 0;
+}
+
+__attribute__((visibility("default"))) void dih_quant_residency_prepare(void *) {}
+
+__attribute__((visibility("default"))) void *dih_quant_matrix_create(void *ctx, int experts, int rows,
+                                                                     int columns, int bits, int group,
+                                                                     char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || experts < 1 || experts > 256 || rows < 1 || columns < 64 || columns > 8192 ||
+        (bits != 5 && bits != 8) || group != 64 || columns % 64) {
+        set_error(error, capacity, "Unsupported quantized matrix shape");
+        return nullptr;
+    }
+    auto *m = new (std::nothrow) Matrix();
+    if (!m) {
+        set_error(error, capacity, "Out of host memory");
+        return nullptr;
+    }
+    m->ctx = c;
+    m->experts = experts; m->rows = rows; m->columns = columns; m->bits = bits;
+    const size_t er = (size_t)experts * rows;
+    m->bytes[0] = er * columns * bits / 8;
+    m->bytes[1] = m->bytes[2] = er * (columns / 64) * 2;
+    for (int i = 0; i < 3; i++) {
+        if (hipMalloc(&m->dev[i], m->bytes[i]) != hipSuccess || hipMemset(m->dev[i], 0, m->bytes[i]) != hipSuccess) {
+            for (int j = 0; j <= i; j++)
+                if (m->dev[j]) (void)hipFree(m->dev[j]);
+            delete m;
+            set_error(error, capacity, "Quantized buffer allocation failed");
+            return nullptr;
+        }
+    }
+    c->weight_bytes += m->bytes[0] + m->bytes[1] + m->bytes[2];
+    return m;
+}
+
+__attribute__((visibility("default"))) void *dih_quant_matrix_buffer(void *matrix, int index) {
+    Matrix *m = as_mat(matrix);
+    if (!m || index < 0 || index > 2) return nullptr;
+    if (!m->host[index]) {
+        void *h = nullptr;
+        if (hipHostMalloc(&h, m->bytes[index], hipHostMallocDefault) != hipSuccess) return nullptr;
+        if (hipMemcpy(h, m->dev[index], m->bytes[index], hipMemcpyDeviceToHost) != hipSuccess) {
+            (void)hipHostFree(h);
+            return nullptr;
+        }
+        m->host[index] = h;
+    }
+    m->dirty[index] = true;
+    return m->host[index];
+}
+
+__attribute__((visibility("default"))) void dih_quant_matrix_destroy(void *matrix) {
+    Matrix *m = as_mat(matrix);
+    if (!m) return;
+    (void)hipDeviceSynchronize();
+    if (m->ctx) m->ctx->weight_bytes -= m->bytes[0] + m->bytes[1] + m->bytes[2];
+    for (int i = 0; i < 3; i++) {
+        if (m->dev[i]) (void)hipFree(m->dev[i]);
+        if (m->host[i]) (void)hipHostFree(m->host[i]);
+    }
+    if (m->stage_in) (void)hipFree(m->stage_in);
+    if (m->stage_out) (void)hipFree(m->stage_out);
+    m->magic = 0;
+    delete m;
+}
+
+__attribute__((visibility("default"))) int dih_quant_matrix_write(void *matrix, int index, size_t offset,
+                                                                  const void *source, size_t bytes,
+                                                                  char *error, int capacity) {
+    Matrix *m = as_mat(matrix);
+    if (!m || index < 0 || index > 2 || !source || offset > m->bytes[index] ||
+        bytes > m->bytes[index] - offset) {
+        set_error(error, capacity, "Invalid quantized buffer write");
+        return -1;
+    }
+    if (!sync_matrix(m, error, capacity)) return -1;
+    if (!hip_ok(hipMemcpy(static_cast<char *>(m->dev[index]) + offset, source, bytes, hipMemcpyDefault),
+                error, capacity, "weight upload"))
+        return -1;
+    if (m->host[index] && hipMemcpy(static_cast<char *>(m->host[index]) + offset, static_cast<char *>(m->dev[index]) + offset,
+                                     bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+        set_error(error, capacity, "staging refresh failed");
+        return -1;
+    }
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_quant_matrix_commit(void *matrix, char *error, int capacity) {
+    Matrix *m = as_mat(matrix);
+    if (!m) {
+        set_error(error, capacity, "Invalid matrix");
+        return -1;
+    }
+    if (!sync_matrix(m, error, capacity)) return -1;
+    for (int i = 0; i < 3; i++)
+        if (m->host[i]) {
+            (void)hipHostFree(m->host[i]);
+            m->host[i] = nullptr;
+        }
+    return 0;
+}
+
+__attribute__((visibility("default"))) void *dih_quant_matrix_device(void *matrix, int index) {
+    Matrix *m = as_mat(matrix);
+    if (!m || index < 0 || index > 2) return nullptr;
+    char err[8];
+    if (!sync_matrix(m, err, sizeof(err))) return nullptr;
+    return m->dev[index];
+}
+
+__attribute__((visibility("default"))) int dih_quant_matrix_shape(void *matrix, int *experts, int *rows,
+                                                                  int *columns, int *bits) {
+    Matrix *m = as_mat(matrix);
+    if (!m) return -1;
+    if (experts) *experts = m->experts;
+    if (rows) *rows = m->rows;
+    if (columns) *columns = m->columns;
+    if (bits) *bits = m->bits;
+    return 0;
+}
+
+// ---------------------------------------------------------------- host-pointer compute
+
+__attribute__((visibility("default"))) int dih_quant_batch(void *ctx, const dih_job *jobs, int count,
+                                                           double *ms, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !jobs || count < 1 || count > 8) {
+        set_error(error, capacity, "Invalid GEMV batch");
+        return -1;
+    }
+    for (int j = 0; j < count; j++) {
+        const dih_job &job = jobs[j];
+        Matrix *m = as_mat(job.matrix);
+        if (!m || m->ctx != c || !job.input || !job.output || !job.experts || job.count < 1 || job.count > 8) {
+            set_error(error, capacity, "Invalid quantized GEMV arguments");
+            return -1;
+        }
+        for (int i = 0; i < job.count; i++)
+            if (job.experts[i] >= (uint32_t)m->experts) {
+                set_error(error, capacity, "Expert ID out of bounds");
+                return -1;
+            }
+        for (int i = 0; i < j; i++)
+            if (jobs[i].matrix == job.matrix) {
+                set_error(error, capacity, "Batch matrices must be distinct");
+                return -1;
+            }
+    }
+    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
+    if (!ids) return -1;
+    hipStream_t s = c->stream;
+    for (int j = 0; j < count; j++) {
+        Matrix *m = as_mat(jobs[j].matrix);
+        size_t in_f = (size_t)m->columns * (jobs[j].batched ? jobs[j].count : 1);
+        if (!sync_matrix(m, error, capacity) || !stage(m, in_f, (size_t)m->rows * jobs[j].count, error, capacity))
+            return -1;
+        if (!hip_ok(hipMemcpyAsync(m->stage_in, jobs[j].input, in_f * 4, hipMemcpyHostToDevice, s), error,
+                    capacity, "input upload") ||
+            !hip_ok(hipMemcpyAsync(ids + 8 * j, jobs[j].experts, jobs[j].count * 4, hipMemcpyHostToDevice, s),
+                    error, capacity, "id upload"))
+            return -1;
+    }
+    (void)hipEventRecord(c->start, s);
+    // Jobs of equal bit width and chunk layout share one launch (up to four per launch).
+    bool done[8] = {false};
+    for (int j = 0; j < count; j++) {
+        if (done[j]) continue;
+        Matrix *mj = as_mat(jobs[j].matrix);
+        QmvSeg segs[4];
+        int n = 0;
+        for (int k = j; k < count && n < 4; k++) {
+            Matrix *mk = as_mat(jobs[k].matrix);
+            if (done[k] || mk->bits != mj->bits || cpl_of(mk->columns) != cpl_of(mj->columns)) continue;
+            QmvSeg sg = seg_of(mk);
+            sg.ids = ids + 8 * k;
+            sg.count = jobs[k].count;
+            sg.x = mk->stage_in;
+            sg.x_bf16 = 0;
+            sg.x_slot_stride = jobs[k].batched ? mk->columns : 0;
+            sg.y = mk->stage_out;
+            segs[n++] = sg;
+            done[k] = true;
+        }
+        if (!launch_qmv(segs, n, mj->bits, nullptr, s, error, capacity)) return -1;
+    }
+    (void)hipEventRecord(c->stop, s);
+    if (!hip_ok(hipStreamSynchronize(s), error, capacity, "Quantized HIP command failed")) return -1;
+    float elapsed = 0;
+    (void)hipEventElapsedTime(&elapsed, c->start, c->stop);
+    if (ms) *ms = elapsed;
+    for (int j = 0; j < count; j++) {
+        Matrix *m = as_mat(jobs[j].matrix);
+        if (!hip_ok(hipMemcpy(jobs[j].output, m->stage_out, (size_t)m->rows * jobs[j].count * 4,
+                              hipMemcpyDeviceToHost),
+                    error, capacity, "output download"))
+            return -1;
+    }
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_quant_matvec(void *ctx, void *matrix, const float *x,
+                                                            float *out, const uint32_t *experts, int count,
+                                                            int batched, double *ms, char *error,
+                                                            int capacity) {
+    dih_job job{matrix, x, out, experts, count, batched};
+    return dih_quant_batch(ctx, &job, 1, ms, error, capacity);
+}
+
+__attribute__((visibility("default"))) int dih_quant_experts(void *ctx, void *gate_, void *up_, void *down_,
+                                                             void *shared_, const float *input,
+                                                             const float *sharedInput,
+                                                             const uint32_t *experts, int count,
+                                                             float *expertOutput, float *sharedOutput,
+                                                             double *ms, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    Matrix *gate = as_mat(gate_), *up = as_mat(up_), *down = as_mat(down_), *shared = as_mat(shared_);
+    if (!c || !gate || !up || !down || !shared || !input || !sharedInput || !experts || !expertOutput ||
+        !sharedOutput || count < 1 || count > 8 || gate == up || gate == down || gate == shared ||
+        up == down || up == shared || down == shared || gate->ctx != c || up->ctx != c ||
+        down->ctx != c || shared->ctx != c || gate->rows != up->rows || gate->columns != up->columns ||
+        gate->experts != up->experts || gate->bits != up->bits || down->experts != gate->experts ||
+        down->columns != gate->rows || down->rows != gate->columns || shared->experts != 1 ||
+        shared->rows != down->rows) {
+        set_error(error, capacity, "Incompatible fused expert matrices/arguments");
+        return -1;
+    }
+    for (int i = 0; i < count; i++)
+        if (experts[i] >= (uint32_t)gate->experts) {
+            set_error(error, capacity, "Expert ID out of bounds");
+            return -1;
+        }
+    hipStream_t s = c->stream;
+    const int I = gate->rows, H = down->rows;
+    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
+    float *act = static_cast<float *>(scratch(c, S_ACT, (size_t)8 * I * 4, error, capacity));
+    if (!ids || !act) return -1;
+    if (!sync_matrix(gate, error, capacity) || !sync_matrix(up, error, capacity) ||
+        !sync_matrix(down, error, capacity) || !sync_matrix(shared, error, capacity) ||
+        !stage(gate, gate->columns, 1, error, capacity) ||
+        !stage(down, 1, (size_t)H * count, error, capacity) ||
+        !stage(shared, shared->columns, H, error, capacity))
+        return -1;
+    if (!hip_ok(hipMemcpyAsync(gate->stage_in, input, (size_t)gate->columns * 4, hipMemcpyHostToDevice, s),
+                error, capacity, "input upload") ||
+        !hip_ok(hipMemcpyAsync(shared->stage_in, sharedInput, (size_t)shared->columns * 4,
+                               hipMemcpyHostToDevice, s),
+                error, capacity, "input upload") ||
+        !hip_ok(hipMemcpyAsync(ids, experts, count * 4, hipMemcpyHostToDevice, s), error, capacity, "id upload"))
+        return -1;
+    (void)hipEventRecord(c->start, s);
+    QmvSeg gu = seg_of(gate);
+    gu.p1 = up->packed(); gu.s1 = up->scales(); gu.b1 = up->biases();
+    gu.ids = ids; gu.count = count; gu.x = gate->stage_in; gu.y = act;
+    if (!launch_qmv(&gu, 1, gate->bits, nullptr, s, error, capacity)) return -1;
+    QmvSeg dn = seg_of(down);
+    dn.ids = ids; dn.count = count; dn.x = act; dn.x_slot_stride = I; dn.y = down->stage_out;
+    QmvSeg sh = seg_of(shared);
+    sh.x = shared->stage_in; sh.y = shared->stage_out;
+    if (down->bits == shared->bits && cpl_of(down->columns) == cpl_of(shared->columns)) {
+        QmvSeg both[2] = {dn, sh};
+        if (!launch_qmv(both, 2, down->bits, nullptr, s, error, capacity)) return -1;
+    } else {
+        if (!launch_qmv(&dn, 1, down->bits, nullptr, s, error, capacity) ||
+            !launch_qmv(&sh, 1, shared->bits, nullptr, s, error, capacity))
+            return -1;
+    }
+    (void)hipEventRecord(c->stop, s);
+    if (!hip_ok(hipStreamSynchronize(s), error, capacity, "Quantized HIP command failed")) return -1;
+    float elapsed = 0;
+    (void)hipEventElapsedTime(&elapsed, c->start, c->stop);
+    if (ms) *ms = elapsed;
+    if (!hip_ok(hipMemcpy(expertOutput, down->stage_out, (size_t)H * count * 4, hipMemcpyDeviceToHost), error,
+                capacity, "output download") ||
+        !hip_ok(hipMemcpy(sharedOutput, shared->stage_out, (size_t)H * 4, hipMemcpyDeviceToHost), error,
+                capacity, "output download"))
+        return -1;
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_quant_embedding(void *matrix, int token, float *out) {
+    Matrix *m = as_mat(matrix);
+    if (!m || !out || token < 0 || token >= m->rows || m->experts != 1) return -1;
+    char err[256];
+    Context *c = m->ctx;
+    float *dev = static_cast<float *>(scratch(c, S_STAGE_Y, (size_t)m->columns * 4, err, sizeof(err)));
+    if (!dev || !sync_matrix(m, err, sizeof(err))) return -1;
+    if (!launch_embedding(m, token, dev, c->stream, err, sizeof(err))) return -1;
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return -1;
+    if (hipMemcpy(out, dev, (size_t)m->columns * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return 0;
+}
+
+// ---------------------------------------------------------------- device-resident path
+
+__attribute__((visibility("default"))) int dih_qmv(void *ctx, void *matrix, const void *x, int x_dtype, void *y,
+                                                   int y_dtype, const uint32_t *experts, int count,
+                                                   int batched, void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    Matrix *m = as_mat(matrix);
+    if (!c || !m || m->ctx != c || !x || !y || count < 1 || count > 8 || (x_dtype != DIH_F32 && x_dtype != DIH_BF16) ||
+        (y_dtype != DIH_F32 && y_dtype != DIH_BF16) || (!experts && count != 1)) {
+        set_error(error, capacity, "Invalid qmv arguments");
+        return -1;
+    }
+    if (!sync_matrix(m, error, capacity)) return -1;
+    QmvSeg sg = seg_of(m);
+    sg.ids = experts; sg.count = count; sg.x = x; sg.x_bf16 = x_dtype == DIH_BF16;
+    sg.x_slot_stride = batched ? m->columns : 0; sg.y = y; sg.y_bf16 = y_dtype == DIH_BF16;
+    hipStream_t s = pick(c, stream);
+    prof_begin(c, s);
+    bool ok = launch_qmv(&sg, 1, m->bits, nullptr, s, error, capacity);
+    prof_mark(c, s, "qmv");
+    return ok ? 0 : -1;
+}
+
+__attribute__((visibility("default"))) int dih_qmv_swiglu(void *ctx, void *gate_, void *up_, const void *x,
+                                                          int x_dtype, float *act, const uint32_t *experts,
+                                                          int count, void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    Matrix *gate = as_mat(gate_), *up = as_mat(up_);
+    if (!c || !gate || !up || gate == up || gate->ctx != c || up->ctx != c || gate->rows != up->rows ||
+        gate->columns != up->columns || gate->experts != up->experts || gate->bits != up->bits || !x || !act ||
+        count < 1 || count > 8 || (!experts && count != 1) || (x_dtype != DIH_F32 && x_dtype != DIH_BF16)) {
+        set_error(error, capacity, "Invalid SwiGLU GEMV arguments");
+        return -1;
+    }
+    if (!sync_matrix(gate, error, capacity) || !sync_matrix(up, error, capacity)) return -1;
+    QmvSeg sg = seg_of(gate);
+    sg.p1 = up->packed(); sg.s1 = up->scales(); sg.b1 = up->biases();
+    sg.ids = experts; sg.count = count; sg.x = x; sg.x_bf16 = x_dtype == DIH_BF16; sg.y = act;
+    hipStream_t s = pick(c, stream);
+    prof_begin(c, s);
+    bool ok = launch_qmv(&sg, 1, gate->bits, nullptr, s, error, capacity);
+    prof_mark(c, s, "qmv_swiglu");
+    return ok ? 0 : -1;
+}
+
+__attribute__((visibility("default"))) int dih_argmax(void *ctx, const float *values, int n, uint32_t *next,
+                                                      void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !values || !next || n < 1) {
+        set_error(error, capacity, "Invalid argmax arguments");
+        return -1;
+    }
+    const size_t parts = (size_t)(n + 1023) / 1024;
+    float *pv = static_cast<float *>(scratch(c, S_ARGVAL, parts * 4, error, capacity));
+    uint32_t *pi = static_cast<uint32_t *>(scratch(c, S_ARGIDX, parts * 4, error, capacity));
+    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
+    if (!pv || !pi || !tk) return -1;
+    hipStream_t s = pick(c, stream);
+    return launch_argmax(values, n, pv, pi, tk + 1, next, s, error, capacity) ? 0 : -1;
+}
+
+__attribute__((visibility("default"))) int dih_lm_head(void *ctx, void *const *slices, int slice_count,
+                                                       const void *x, float *logits, uint32_t *next,
+                                                       void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !slices || slice_count < 1 || slice_count > 64 || !x || !logits || !next) {
+        set_error(error, capacity, "Invalid lm_head arguments");
+        return -1;
+    }
+    Matrix *first = as_mat(slices[0]);
+    long total = 0;
+    for (int i = 0; i < slice_count; i++) {
+        Matrix *m = as_mat(slices[i]);
+        if (!m || !first || m->ctx != c || m->experts != 1 || m->columns != first->columns || m->bits != first->bits) {
+            set_error(error, capacity, "lm_head slices must be single-expert matrices of equal width and bits");
+            return -1;
+        }
+        total += m->rows;
+    }
+    if (total > 0x7fffffffL) {
+        set_error(error, capacity, "Vocabulary too large");
+        return -1;
+    }
+    for (int i = 0; i < slice_count; i++)
+        if (!sync_matrix(as_mat(slices[i]), error, capacity)) return -1;
+    const size_t parts = (size_t)(total + 1023) / 1024;
+    float *pv = static_cast<float *>(scratch(c, S_ARGVAL, parts * 4, error, capacity));
+    uint32_t *pi = static_cast<uint32_t *>(scratch(c, S_ARGIDX, parts * 4, error, capacity));
+    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
+    if (!pv || !pi || !tk) return -1;
+    hipStream_t s = pick(c, stream);
+    prof_begin(c, s);
+    long offset = 0;
+    for (int i = 0; i < slice_count; i += 4) {
+        QmvSeg segs[4];
+        int n = 0;
+        for (int k = i; k < slice_count && k < i + 4; k++) {
+            Matrix *m = as_mat(slices[k]);
+            QmvSeg sg = seg_of(m);
+            sg.x = x; sg.x_bf16 = 1; sg.y = logits + offset;
+            offset += m->rows;
+            segs[n++] = sg;
+        }
+        if (!launch_qmv(segs, n, first->bits, nullptr, s, error, capacity)) return -1;
+    }
+    prof_mark(c, s, "lm_head_qmv");
+    if (!launch_argmax(logits, (int)total, pv, pi, tk + 1, next, s, error, capacity)) return -1;
+    prof_mark(c, s, "argmax");
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_top8(void *ctx, const void *logits, int logits_dtype, int tokens,
+                                                    int experts, uint32_t *ids, float *probs, uint32_t *status,
+                                                    void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !logits || !ids || !probs || tokens < 1 || experts < 8 || experts > 256 ||
+        (logits_dtype != DIH_F32 && logits_dtype != DIH_BF16)) {
+        set_error(error, capacity, "Invalid router selection arguments");
+        return -1;
+    }
+    return launch_top8(logits, logits_dtype == DIH_BF16, tokens, experts, ids, probs, status, nullptr,
+                       nullptr, pick(c, stream), error, capacity)
+               ? 0
+               : -1;
+}
+
+static size_t max_chunks_for(int tokens, int experts, int with_shared) {
+    size_t routed = (size_t)tokens * 8;
+    return (routed + 63) / 64 + std::min<size_t>((size_t)experts, routed) +
+           (with_shared ? ((size_t)tokens + 63) / 64 : 0);
+}
+
+__attribute__((visibility("default"))) int dih_build_groups(void *ctx, const uint32_t *ids, int tokens,
+                                                            int experts, uint32_t *counts, uint32_t *routes,
+                                                            void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !ids || !counts || !routes || tokens < 1 || experts < 1 || experts > 256) {
+        set_error(error, capacity, "Invalid grouping arguments");
+        return -1;
+    }
+    int4 *chunks = static_cast<int4 *>(scratch(c, S_CHUNKS, max_chunks_for(tokens, experts, 0) * 16, error, capacity));
+    uint32_t *nch = static_cast<uint32_t *>(scratch(c, S_NCHUNKS, 16, error, capacity));
+    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
+    if (!chunks || !nch || !tk) return -1;
+    return launch_build_groups(ids, tokens, experts, 0, counts, routes, chunks, nch, tk + 2, pick(c, stream), error,
+                               capacity)
+               ? 0
+               : -1;
+}
+
+__attribute__((visibility("default"))) int dih_dequant_bf16(void *ctx, void *matrix, int expert, uint16_t *out,
+                                                            void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    Matrix *m = as_mat(matrix);
+    if (!c || !m || m->ctx != c || !out || expert < 0 || expert >= m->experts) {
+        set_error(error, capacity, "Invalid dequantize arguments");
+        return -1;
+    }
+    if (!sync_matrix(m, error, capacity)) return -1;
+    return launch_dequant_bf16(m, expert, out, pick(c, stream), error, capacity) ? 0 : -1;
+}
+
+static bool check_layer(Context *c, const dih_moe_layer *L, bool need_router, int *E, int *H, int *I, int *Is,
+                        char *error, int capacity) {
+    if (!L) {
+        set_error(error, capacity, "Missing MoE layer");
+        return false;
+    }
+    Matrix *gate = as_mat(L->gate), *up = as_mat(L->up), *down = as_mat(L->down);
+    Matrix *sg = as_mat(L->shared_gate), *su = as_mat(L->shared_up), *sd = as_mat(L->shared_down);
+    Matrix *sr = as_mat(L->shared_route), *router = as_mat(L->router);
+    if (!gate || !up || !down || !sg || !su || !sd || !sr || (need_router && !router) || (L->router && !router)) {
+        set_error(error, capacity, "Incomplete MoE layer");
+        return false;
+    }
+    Matrix *all[8] = {gate, up, down, sg, su, sd, sr, router};
+    for (Matrix *m : all)
+        if (m && m->ctx != c) {
+            set_error(error, capacity, "MoE matrices must belong to this context");
+            return false;
+        }
+    *E = gate->experts; *H = gate->columns; *I = gate->rows; *Is = sg->rows;
+    if (up->experts != *E || up->rows != *I || up->columns != *H || up->bits != gate->bits ||
+        down->experts != *E || down->rows != *H || down->columns != *I || down->bits != gate->bits ||
+        sg->experts != 1 || su->experts != 1 || su->rows != *Is || sg->columns != *H || su->columns != *H ||
+        su->bits != sg->bits || sd->experts != 1 || sd->rows != *H || sd->columns != *Is ||
+        sr->experts != 1 || sr->rows != 1 || sr->columns != *H || *E < 8 ||
+        (router && (router->experts != 1 || router->rows != *E || router->columns != *H)) || *I > 2048 ||
+        *Is > 2048 || (*H % 64) != 0) {
+        set_error(error, capacity, "Incompatible MoE layer shapes");
+        return false;
+    }
+    for (Matrix *m : all)
+        if (m && !sync_matrix(m, error, capacity)) return false;
+    return true;
+}
+
+__attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_moe_layer *L, const void *x,
+                                                          const float *logits, void *residual,
+                                                          const dih_moe_trace *trace, void *stream, char *error,
+                                                          int capacity) {
+    Context *c = as_ctx(ctx);
+    int E, H, I, Is;
+    if (!c || !x || !residual) {
+        set_error(error, capacity, "Invalid decode MoE arguments");
+        return -1;
+    }
+    if (!check_layer(c, L, logits == nullptr, &E, &H, &I, &Is, error, capacity)) return -1;
+    if (logits && L->router) {
+        set_error(error, capacity, "Pass either a router matrix or logits, not both");
+        return -1;
+    }
+    Matrix *gate = as_mat(L->gate), *up = as_mat(L->up), *down = as_mat(L->down);
+    Matrix *sg = as_mat(L->shared_gate), *su = as_mat(L->shared_up), *sd = as_mat(L->shared_down);
+    Matrix *sr = as_mat(L->shared_route), *router = as_mat(L->router);
+    float *lg = static_cast<float *>(scratch(c, S_LOGITS, (size_t)E * 4, error, capacity));
+    float *srt = static_cast<float *>(scratch(c, S_SROUTE, 16, error, capacity));
+    float *sact = static_cast<float *>(scratch(c, S_SACT, (size_t)Is * 4, error, capacity));
+    float *act = static_cast<float *>(scratch(c, S_ACT, (size_t)8 * I * 4, error, capacity));
+    float *sout = static_cast<float *>(scratch(c, S_SOUT, (size_t)H * 4, error, capacity));
+    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
+    float *probs = static_cast<float *>(scratch(c, S_PROBS, 8 * 4, error, capacity));
+    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
+    uint32_t *status = static_cast<uint32_t *>(scratch(c, S_STATUS, 16, error, capacity));
+    if (!lg || !srt || !sact || !act || !sout || !ids || !probs || !tk || !status) return -1;
+    hipStream_t s = pick(c, stream);
+    prof_begin(c, s);
+    const float *use_logits = logits ? logits : lg;
+    // Stage 1: router logits, shared-expert gate GEMV and shared gate/up SwiGLU share x;
+    // the last block of the launch that holds the router selects the experts.
+    QmvSeg s1[3];
+    int n8 = 0;
+    Top8Epilogue tp;
+    tp.logits = use_logits; tp.experts = E; tp.ids = ids; tp.probs = probs; tp.status = trace ? trace->status : nullptr;
+    tp.ticket = tk;
+    if (router) {
+        QmvSeg a = seg_of(router);
+        a.x = x; a.x_bf16 = 1; a.y = lg;
+        s1[n8++] = a;
+    }
+    QmvSeg b = seg_of(sr);
+    b.x = x; b.x_bf16 = 1; b.y = srt;
+    QmvSeg g = seg_of(sg);
+    g.p1 = su->packed(); g.s1 = su->scales(); g.b1 = su->biases(); g.x = x; g.x_bf16 = 1; g.y = sact;
+    // Group segments by bit width (router and shared_route are 8-bit; experts may be 5-bit).
+    QmvSeg rest[2];
+    int nrest = 0;
+    if (sr->bits == 8) s1[n8++] = b; else rest[nrest++] = b;
+    if (sg->bits == 8) s1[n8++] = g; else rest[nrest++] = g;
+    if (n8 && !launch_qmv(s1, n8, 8, &tp, s, error, capacity)) return -1;
+    if (nrest && !launch_qmv(rest, nrest, 5, n8 ? nullptr : &tp, s, error, capacity)) return -1;
+    prof_mark(c, s, "decode_router_shared");
+    // Stage 2: selected experts' gate/up SwiGLU and the shared down projection.
+    QmvSeg e2 = seg_of(gate);
+    e2.p1 = up->packed(); e2.s1 = up->scales(); e2.b1 = up->biases();
+    e2.ids = ids; e2.count = 8; e2.x = x; e2.x_bf16 = 1; e2.y = act;
+    QmvSeg d2 = seg_of(sd);
+    d2.x = sact; d2.y = sout;
+    if (sd->bits == gate->bits && cpl_of(sd->columns) == cpl_of(gate->columns)) {
+        QmvSeg both[2] = {e2, d2};
+        if (!launch_qmv(both, 2, gate->bits, nullptr, s, error, capacity)) return -1;
+    } else {
+        if (!launch_qmv(&e2, 1, gate->bits, nullptr, s, error, capacity) ||
+            !launch_qmv(&d2, 1, sd->bits, nullptr, s, error, capacity))
+            return -1;
+    }
+    prof_mark(c, s, "decode_experts_gate_up");
+    // Stage 3: expert down projections and the weighted merge into the residual.
+    if (!launch_moe_down_merge(down, act, ids, probs, sout, srt, static_cast<uint16_t *>(residual),
+                               trace ? trace->expert_out : nullptr, s, error, capacity))
+        return -1;
+    prof_mark(c, s, "decode_down_merge");
+    if (trace) {
+        if (trace->logits && !hip_ok(hipMemcpyAsync(trace->logits, use_logits, (size_t)E * 4, hipMemcpyDeviceToDevice, s),
+                                     error, capacity, "trace copy"))
+            return -1;
+        if (trace->ids && !hip_ok(hipMemcpyAsync(trace->ids, ids, 32, hipMemcpyDeviceToDevice, s), error, capacity,
+                                  "trace copy"))
+            return -1;
+        if (trace->probs && !hip_ok(hipMemcpyAsync(trace->probs, probs, 32, hipMemcpyDeviceToDevice, s), error,
+                                    capacity, "trace copy"))
+            return -1;
+    }
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_moe_prefill(void *ctx, const dih_moe_layer *L, int tokens,
+                                                           const void *x, const void *logits, int logits_dtype,
+                                                           void *residual, const dih_moe_trace *trace,
+                                                           void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    int E, H, I, Is;
+    if (!c || !x || !logits || !residual || tokens < 1 || tokens > (1 << 20) ||
+        (logits_dtype != DIH_F32 && logits_dtype != DIH_BF16)) {
+        set_error(error, capacity, "Invalid prefill MoE arguments");
+        return -1;
+    }
+    if (!check_layer(c, L, false, &E, &H, &I, &Is, error, capacity)) return -1;
+    Matrix *gate = as_mat(L->gate), *up = as_mat(L->up), *down = as_mat(L->down);
+    Matrix *sg = as_mat(L->shared_gate), *su = as_mat(L->shared_up), *sd = as_mat(L->shared_down);
+    Matrix *sr = as_mat(L->shared_route);
+    if (Is != I || sg->bits != gate->bits || sd->bits != gate->bits) {
+        set_error(error, capacity, "Grouped prefill needs the shared expert to match the routed experts' shape and bits");
+        return -1;
+    }
+    const size_t T = (size_t)tokens, routes_n = T * 9;
+    const size_t maxc = max_chunks_for(tokens, E, 1);
+    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, std::max<size_t>(T * 8 * 4, 256), error, capacity));
+    float *probs = static_cast<float *>(scratch(c, S_PROBS, T * 8 * 4, error, capacity));
+    uint32_t *counts = static_cast<uint32_t *>(scratch(c, S_COUNTS, (size_t)(E + 1) * 4, error, capacity));
+    uint32_t *routes = static_cast<uint32_t *>(scratch(c, S_ROUTES, (size_t)(E + 1) * T * 4, error, capacity));
+    int4 *chunks = static_cast<int4 *>(scratch(c, S_CHUNKS, maxc * 16, error, capacity));
+    uint32_t *nch = static_cast<uint32_t *>(scratch(c, S_NCHUNKS, 16, error, capacity));
+    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
+    uint16_t *actb = static_cast<uint16_t *>(scratch(c, S_ACTBF, routes_n * I * 2, error, capacity));
+    float *rout = static_cast<float *>(scratch(c, S_ROUTEOUT, routes_n * H * 4, error, capacity));
+    if (!ids || !probs || !counts || !routes || !chunks || !nch || !tk || !actb || !rout) return -1;
+    float *route_out = trace && trace->expert_out ? trace->expert_out : rout;
+    hipStream_t s = pick(c, stream);
+    prof_begin(c, s);
+    if (!launch_top8(logits, logits_dtype == DIH_BF16, tokens, E, ids, probs, trace ? trace->status : nullptr,
+                     trace ? trace->logits : nullptr, tk + 3, s, error, capacity))
+        return -1;
+    prof_mark(c, s, "prefill_top8");
+    if (!launch_build_groups(ids, tokens, E, 1, counts, routes, chunks, nch, tk + 3, s, error, capacity)) return -1;
+    prof_mark(c, s, "prefill_group");
+    QmmArgs a;
+    a.m0 = gate; a.m1 = up; a.sm0 = sg; a.sm1 = su; a.tokens = tokens; a.routes = routes; a.chunks = chunks;
+    a.nchunks = nch; a.max_chunks = (int)maxc; a.x = static_cast<const uint16_t *>(x); a.in_mode = 1;
+    a.y = actb; a.y_bf16 = 1;
+    if (!launch_qmm(a, s, error, capacity)) return -1;
+    prof_mark(c, s, "prefill_gate_up");
+    QmmArgs d;
+    d.m0 = down; d.sm0 = sd; d.tokens = tokens; d.routes = routes; d.chunks = chunks; d.nchunks = nch;
+    d.max_chunks = (int)maxc; d.x = actb; d.in_mode = 0; d.y = route_out; d.y_bf16 = 0;
+    if (!launch_qmm(d, s, error, capacity)) return -1;
+    prof_mark(c, s, "prefill_down");
+    if (!launch_moe_merge(sr, static_cast<const uint16_t *>(x), tokens, H, route_out, probs,
+                          static_cast<uint16_t *>(residual), s, error, capacity))
+        return -1;
+    prof_mark(c, s, "prefill_merge");
+    if (trace) {
+        if (trace->ids && !hip_ok(hipMemcpyAsync(trace->ids, ids, T * 32, hipMemcpyDeviceToDevice, s), error,
+                                  capacity, "trace copy"))
+            return -1;
+        if (trace->probs && !hip_ok(hipMemcpyAsync(trace->probs, probs, T * 32, hipMemcpyDeviceToDevice, s), error,
+                                    capacity, "trace copy"))
+            return -1;
+    }
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_dense(void *ctx, void *matrix, int tokens, const void *x, void *y,
+                                                     int y_dtype, void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    Matrix *m = as_mat(matrix);
+    if (!c || !m || m->ctx != c || m->experts != 1 || tokens < 1 || !x || !y ||
+        (y_dtype != DIH_F32 && y_dtype != DIH_BF16)) {
+        set_error(error, capacity, "Invalid dense projection arguments");
+        return -1;
+    }
+    if (!sync_matrix(m, error, capacity)) return -1;
+    QmmArgs a;
+    a.m0 = m; a.tokens = tokens; a.dense = 1; a.x = static_cast<const uint16_t *>(x); a.in_mode = 0;
+    a.y = y; a.y_bf16 = y_dtype == DIH_BF16;
+    hipStream_t s = pick(c, stream);
+    prof_begin(c, s);
+    bool ok = launch_qmm(a, s, error, capacity);
+    prof_mark(c, s, "dense_qmm");
+    return ok ? 0 : -1;
+}
+
+__attribute__((visibility("default"))) int dih_set_profiling(void *ctx, int enabled) {
+    Context *c = as_ctx(ctx);
+    if (!c) return -1;
+    if (c->prof_used && hipDeviceSynchronize() != hipSuccess) return -1;
+    c->profiling = enabled != 0;
+    c->prof_recs.clear();
+    c->prof_used = 0;
+    c->prof_last = -1;
+    return 0;
+}
+
+__attribute__((visibility("default"))) int dih_profile_read(void *ctx, double *total_ms, int *counts,
+                                                            const char **names, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !c->profiling) return 0;
+    if (c->prof_used && hipEventSynchronize(c->prof_pool[c->prof_used - 1]) != hipSuccess) return -1;
+    int n = 0;
+    for (const auto &r : c->prof_recs) {
+        int k = 0;
+        while (k < n && strcmp(names[k], r.name) != 0) k++;
+        if (k == n) {
+            if (n == capacity) continue;
+            names[n] = r.name;
+            total_ms[n] = 0;
+            counts[n] = 0;
+            n++;
+        }
+        float e = 0;
+        (void)hipEventElapsedTime(&e, c->prof_pool[r.begin], c->prof_pool[r.end]);
+        total_ms[k] += e;
+        counts[k] += 1;
+    }
+    return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+// Device helpers shared by the gfx950 kernels: bf16 conversion, MLX-affine code
+// extraction for one lane's 32-code chunk, wave reductions.
+//
+// Lane chunk: the kernels give every lane 32 consecutive codes of one row, i.e. half of
+// one 64-column affine group (one scale, one bias). For 8-bit that is 32 bytes (8 dwords,
+// 32-byte aligned); for 5-bit it is 20 bytes (5 dwords, 4-byte aligned) because two
+// groups occupy exactly 80 bytes. Bit c*bits of the row holds code c LSB-first, and a
+// code may straddle two words (quantized.mm:62-82 restated as an unrolled extraction
+// whose word index and shift are compile-time constants).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DIH_DEV __device__ __forceinline__
+
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short dih_bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float dih_f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float dih_f32x4;
+
+DIH_DEV float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Round-to-nearest-even f32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+DIH_DEV uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+    bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+DIH_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+template <int BITS>
+struct Chunk {
+    uint32_t w[BITS];  // 32 codes * BITS bits = BITS dwords
+};
+
+// Loads the 32-code chunk `chunk` (0-based, 32 columns each) of a row starting at `row`.
+template <int BITS>
+DIH_DEV void load_chunk(Chunk<BITS> &c, const uint32_t *row, int chunk) {
+    const uint32_t *p = row + chunk * BITS;
+    if constexpr (BITS == 8) {
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 *q = reinterpret_cast<const u32x4 *>(p);
+        u32x4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+        c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
+        c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < BITS; i++) c.w[i] = __builtin_nontemporal_load(p + i);
+    }
+}
+
+// Code i (0..31) of a chunk.
+template <int BITS>
+DIH_DEV uint32_t chunk_code(const Chunk<BITS> &c, int i) {
+    const int bit = i * BITS, w = bit >> 5, s = bit & 31;
+    uint32_t v;
+    if (s + BITS <= 32)
+        v = c.w[w] >> s;
+    else
+        v = __builtin_amdgcn_alignbit(c.w[w + 1], c.w[w], s);
+    return v & ((1u << BITS) - 1u);
+}
+
+// sum_i code_i * x_i over the chunk, four independent partial sums.
+template <int BITS>
+DIH_DEV float chunk_dot(const Chunk<BITS> &c, const float *x) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        a0 = fmaf((float)chunk_code<BITS>(c, i + 0), x[i + 0], a0);
+        a1 = fmaf((float)chunk_code<BITS>(c, i + 1), x[i + 1], a1);
+        a2 = fmaf((float)chunk_code<BITS>(c, i + 2), x[i + 2], a2);
+        a3 = fmaf((float)chunk_code<BITS>(c, i + 3), x[i + 3], a3);
+    }
+    return (a0 + a1) + (a2 + a3);
+}
+
+// Dequantize a chunk to bf16 MFMA operands: operand j holds codes 8j..8j+7 as
+// bf16(code*scale + bias) with the fp32 value rounded to nearest even (the reference's
+// bfloat(float(q)*scale+bias), prefill_expert_packed.mm:34).
+template <int BITS>
+DIH_DEV void chunk_to_bf16(const Chunk<BITS> &c, float scale, float bias, dih_bf16x8 (&op)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t p[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float lo = fmaf((float)chunk_code<BITS>(c, 8 * j + 2 * k), scale, bias);
+            float hi = fmaf((float)chunk_code<BITS>(c, 8 * j + 2 * k + 1), scale, bias);
+            p[k] = pack_bf16x2(lo, hi);
+        }
+        op[j] = __builtin_bit_cast(dih_bf16x8, (uint4){p[0], p[1], p[2], p[3]});
+    }
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two, <= 64).
+DIH_DEV float group_sum(float v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+DIH_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+DIH_DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+DIH_DEV uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t w = (uint32_t)__shfl_xor((int)v, o, 64);
+        v = w < v ? w : v;
+    }
+    return v;
+}
+
+DIH_DEV float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
+DIH_DEV float siluf_(float v) { return v * sigmoidf_(v); }
+
+// Loads 32 activations of one chunk as f32 (from f32 or bf16 storage).
+DIH_DEV void load_x32(float *x, const void *base, int x_bf16, int offset) {
+    if (x_bf16) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + offset);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint4 v = p[q];
+            uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                x[8 * q + 2 * k] = __uint_as_float(u[k] << 16);
+                x[8 * q + 2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+            }
+        }
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + offset);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            float4 v = p[q];
+            x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+        }
+    }
+}

@@ -1,0 +1,141 @@
+// Host-side internals of libdeepinfer_hip: context and matrix objects, scratch
+// management, kernel launchers shared between translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/deepinfer_hip.h"
+
+namespace dih {
+
+struct Context;
+
+// One MLX-affine matrix [experts, rows, columns] (QMatrix, quantized.mm:16-20).
+struct Matrix {
+    Context *ctx = nullptr;
+    int experts = 0, rows = 0, columns = 0, bits = 0;
+    void *dev[3] = {nullptr, nullptr, nullptr};   // packed, scales, biases (device)
+    void *host[3] = {nullptr, nullptr, nullptr};  // pinned staging (lazy)
+    bool dirty[3] = {false, false, false};
+    size_t bytes[3] = {0, 0, 0};
+    float *stage_in = nullptr, *stage_out = nullptr;  // f32 staging for host-pointer calls
+    size_t stage_in_bytes = 0, stage_out_bytes = 0;
+    uint32_t magic = 0x44494d58u;
+
+    const uint32_t *packed() const { return static_cast<const uint32_t *>(dev[0]); }
+    const uint16_t *scales() const { return static_cast<const uint16_t *>(dev[1]); }
+    const uint16_t *biases() const { return static_cast<const uint16_t *>(dev[2]); }
+    size_t words_per_row() const { return (size_t)columns * bits / 32; }
+    size_t groups_per_row() const { return (size_t)columns / 64; }
+};
+
+// Grow-only device scratch buffer.
+struct Scratch {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool resident = false;
+    uint64_t weight_bytes = 0;
+    // profiling: events recorded on the call's stream between the stages of every
+    // device-resident call; aggregated per stage name when read
+    bool profiling = false;
+    std::vector<hipEvent_t> prof_pool;        // reused across resets
+    struct ProfRec { int begin, end; const char *name; };
+    std::vector<ProfRec> prof_recs;
+    int prof_used = 0;                        // events taken from the pool since reset
+    int prof_last = -1;                       // event that closes the previous stage
+    // named scratch
+    Scratch ws[24];
+    uint32_t magic = 0x44494358u;
+};
+
+enum ScratchId {
+    S_IDS, S_PROBS, S_STATUS, S_TICKETS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
+    S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
+    S_STAGE_X, S_STAGE_Y, S_COUNT_
+};
+
+// Error helpers (bridge.mm:9-15 convention).
+void set_error(char *error, int capacity, const std::string &message);
+bool hip_ok(hipError_t e, char *error, int capacity, const char *what);
+void *scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity);
+bool sync_matrix(Matrix *m, char *error, int capacity);
+
+// Profiling helpers: stage boundaries on `stream`.
+void prof_begin(Context *c, hipStream_t s);
+void prof_mark(Context *c, hipStream_t s, const char *name);
+
+// ---- launchers (defined in the .hip translation units) ----
+
+// Generic GEMV segment: rows of one matrix (or a gate/up pair for SwiGLU) for
+// `count` slots whose expert ids come from a device array.
+struct QmvSeg {
+    const uint32_t *p0 = nullptr; const uint16_t *s0 = nullptr, *b0 = nullptr;
+    const uint32_t *p1 = nullptr; const uint16_t *s1 = nullptr, *b1 = nullptr;  // SwiGLU up
+    const uint32_t *ids = nullptr;  // device expert ids or null (expert 0)
+    int rows = 0, columns = 0, count = 1;
+    int experts = 1;                // ids >= experts produce NaN outputs (no fault)
+    const void *x = nullptr; int x_bf16 = 0; int x_slot_stride = 0;  // elements
+    void *y = nullptr; int y_bf16 = 0;
+};
+// Launches up to 4 segments of equal bit width in one kernel. `top8` (optional) makes
+// the last finishing block select experts from `top8_logits`.
+struct Top8Epilogue {
+    const float *logits = nullptr; int experts = 0;
+    uint32_t *ids = nullptr; float *probs = nullptr; uint32_t *status = nullptr;
+    uint32_t *ticket = nullptr;
+};
+bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Epilogue *top8,
+                hipStream_t s, char *error, int capacity);
+
+bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t *ids,
+                           const float *probs, const float *shared_out, const float *sroute,
+                           uint16_t *residual, float *route_out, hipStream_t s, char *error,
+                           int capacity);
+
+bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, uint32_t *ids,
+                 float *probs, uint32_t *status, float *logits_copy, uint32_t *zero_word,
+                 hipStream_t s, char *error, int capacity);
+
+bool launch_build_groups(const uint32_t *ids, int tokens, int experts, int with_shared,
+                         uint32_t *counts, uint32_t *routes, int4 *chunks, uint32_t *nchunks,
+                         uint32_t *ticket, hipStream_t s, char *error, int capacity);
+
+struct QmmArgs {
+    // routed matrices (gate or down) and optional up for the gated kernel
+    const Matrix *m0 = nullptr, *m1 = nullptr;
+    // shared-expert matrices used for chunks whose expert == experts
+    const Matrix *sm0 = nullptr, *sm1 = nullptr;
+    int tokens = 0;         // T
+    int dense = 0;          // 1: identity routes over `tokens`, no chunk list
+    const uint32_t *routes = nullptr;   // [(E+1)*T]
+    const int4 *chunks = nullptr;       // (expert, start, n, 0)
+    const uint32_t *nchunks = nullptr;  // device count
+    int max_chunks = 0;
+    const uint16_t *x = nullptr;        // bf16 input rows
+    int in_mode = 0;                    // 0: row = route; 1: gate input row (route/8, shared)
+    void *y = nullptr; int y_bf16 = 0;  // output rows indexed by route
+};
+bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity);
+
+bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens, int hidden,
+                      const float *route_out, const float *probs, uint16_t *residual,
+                      hipStream_t s, char *error, int capacity);
+
+bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
+                   uint32_t *ticket, uint32_t *next, hipStream_t s, char *error, int capacity);
+
+bool launch_dequant_bf16(const Matrix *m, int expert, uint16_t *out, hipStream_t s, char *error,
+                         int capacity);
+bool launch_embedding(const Matrix *m, int token, float *out, hipStream_t s, char *error,
+                      int capacity);
+
+}  // namespace dih

@@ -1,0 +1,293 @@
+// MoE routing, grouping, merge and argmax kernels (integer/bandwidth work, no MFMA).
+#include "dih_device.h"
+#include "dih_internal.h"
+
+namespace dih {
+
+// ------------------------------------------------------------------------------ top-8
+
+// One wave per token (prefill_top8 gpu_prefill.mm:151-161 / SelectExperts
+// Qwen36Model.cs:246-262): eight rounds of wave max with ties to the lowest expert id,
+// then softmax over the eight chosen logits (largest subtracted, summed in slot order).
+// A non-finite logit sets *status = 1 and the token's ids to 0.
+__global__ __launch_bounds__(256) void top8_kernel(const void *logits, int logits_bf16, int tokens,
+                                                   int experts, uint32_t *ids, float *probs,
+                                                   uint32_t *status, float *logits_copy,
+                                                   uint32_t *zero_word) {
+    if (zero_word && blockIdx.x == 0 && threadIdx.x == 0) *zero_word = 0u;
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    float cand[4];
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        float v = -INFINITY;
+        if (e < experts) {
+            const size_t at = (size_t)t * experts + e;
+            v = logits_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(logits)[at])
+                            : static_cast<const float *>(logits)[at];
+            if (!isfinite(v)) bad = true;
+            if (logits_copy) logits_copy[at] = v;
+        }
+        cand[j] = v;
+    }
+    const bool any_bad = __any(bad);
+    float chosen[8];
+    uint32_t picked[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        float best = cand[0];
+        uint32_t id = (uint32_t)lane;
+#pragma unroll
+        for (int j = 1; j < 4; j++)
+            if (cand[j] > best) { best = cand[j]; id = (uint32_t)(lane + 64 * j); }
+        const float m = wave_max(best);
+        const uint32_t sel = wave_min_u32(best == m ? id : 0xffffffffu);
+        chosen[n] = m;
+        picked[n] = sel;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if ((uint32_t)(lane + 64 * j) == sel) cand[j] = -INFINITY;
+    }
+    if (lane == 0) {
+        float p[8], total = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) { p[i] = __expf(chosen[i] - chosen[0]); total += p[i]; }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            ids[(size_t)t * 8 + i] = any_bad ? 0u : picked[i];
+            probs[(size_t)t * 8 + i] = p[i] / total;
+        }
+        if (any_bad && status) *status = 1u;
+    }
+}
+
+bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, uint32_t *ids,
+                 float *probs, uint32_t *status, float *logits_copy, uint32_t *zero_word,
+                 hipStream_t s, char *error, int capacity) {
+    hipLaunchKernelGGL(top8_kernel, dim3((tokens + 3) / 4), dim3(256), 0, s, logits, logits_bf16,
+                       tokens, experts, ids, probs, status, logits_copy, zero_word);
+    return hip_ok(hipGetLastError(), error, capacity, "top8 launch");
+}
+
+// ------------------------------------------------------------------------- grouping
+
+// Block e lists the routes r (= token*8 + slot) with ids[r] == e in ascending order
+// (prefill_build_groups prefill_moe.mm:8-17 uses a SIMD prefix sum per 32 routes; here a
+// 256-thread ballot/prefix pass per 256 routes). Block `experts` (when with_shared) lists
+// the shared expert's routes T*8 + t for every token. The last block to finish builds the
+// chunk list in expert order: ceil(count/64) chunks per expert, (expert, start, n), which
+// makes the order deterministic where the reference's atomic tile append is not
+// (prefill_moe.mm:15).
+__global__ __launch_bounds__(256) void group_kernel(const uint32_t *ids, int tokens, int experts,
+                                                    int with_shared, uint32_t *counts,
+                                                    uint32_t *routes, int4 *chunks,
+                                                    uint32_t *nchunks, uint32_t *ticket) {
+    __shared__ uint32_t wave_tot[4];
+    __shared__ int last;
+    __shared__ uint32_t scan[257];
+    const int e = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int T8 = tokens * 8;
+    uint32_t *out = routes + (size_t)e * tokens;
+    if (e == experts) {
+        for (int t = tid; t < tokens; t += 256) out[t] = (uint32_t)(T8 + t);
+        if (tid == 0) counts[e] = (uint32_t)tokens;
+    } else {
+        uint32_t total = 0;
+        for (int base = 0; base < T8; base += 256) {
+            const int r = base + tid;
+            const bool sel = r < T8 && ids[r] == (uint32_t)e;
+            const unsigned long long mask = __ballot(sel);
+            const uint32_t below = (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+            if (lane == 0) wave_tot[wave] = (uint32_t)__popcll(mask);
+            __syncthreads();
+            uint32_t off = total;
+            for (int w = 0; w < wave; w++) off += wave_tot[w];
+            // A token lists an expert at most once, so count <= tokens; ids that repeat an
+            // expert within a token are truncated here instead of overrunning the list.
+            if (sel && off + below < (uint32_t)tokens) out[off + below] = (uint32_t)r;
+            total += wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+            __syncthreads();
+        }
+        if (tid == 0) counts[e] = min(total, (uint32_t)tokens);
+    }
+    // last block: chunk list
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = (atomicAdd(ticket, 1u) == gridDim.x - 1);
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const int n = experts + with_shared;  // <= 257
+    for (int i = tid; i < n; i += 256) scan[i] = (counts[i] + 63u) / 64u;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        for (int i = 0; i < n; i++) {
+            uint32_t v = scan[i];
+            scan[i] = acc;
+            acc += v;
+        }
+        *nchunks = acc;
+        *ticket = 0u;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += 256) {
+        const uint32_t c = counts[i];
+        uint32_t at = scan[i];
+        for (uint32_t s = 0; s < c; s += 64, at++)
+            chunks[at] = make_int4(i, (int)s, (int)min(64u, c - s), 0);
+    }
+}
+
+bool launch_build_groups(const uint32_t *ids, int tokens, int experts, int with_shared,
+                         uint32_t *counts, uint32_t *routes, int4 *chunks, uint32_t *nchunks,
+                         uint32_t *ticket, hipStream_t s, char *error, int capacity) {
+    hipLaunchKernelGGL(group_kernel, dim3(experts + with_shared), dim3(256), 0, s, ids, tokens,
+                       experts, with_shared, counts, routes, chunks, nchunks, ticket);
+    return hip_ok(hipGetLastError(), error, capacity, "grouping launch");
+}
+
+// ---------------------------------------------------------------------------- merge
+
+// One block per token (prefill_merge gpu_prefill.mm:140-150 without the next-layer
+// norm): gate = sigmoid(shared_route . x[t]); y = gate*out[T*8+t] + sum_{slot 0..7}
+// p*out[t*8+slot]; residual[t] = bf16(residual[t] + y).
+template <int BITS>
+__global__ __launch_bounds__(256) void merge_kernel(const uint32_t *sr_packed,
+                                                    const uint16_t *sr_scales,
+                                                    const uint16_t *sr_biases,
+                                                    const uint16_t *x, int tokens, int H,
+                                                    const float *route_out, const float *probs,
+                                                    uint16_t *residual) {
+    __shared__ float part[4];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nchunk = H >> 5;
+    float d = 0.f;
+    for (int ch = tid; ch < nchunk; ch += 256) {
+        Chunk<BITS> c;
+        load_chunk<BITS>(c, sr_packed, ch);
+        float xr[32];
+        load_x32(xr, x + (size_t)t * H, 1, ch * 32);
+        float xs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xs += xr[i];
+        d += bf16_to_f32(sr_scales[ch >> 1]) * chunk_dot<BITS>(c, xr) + bf16_to_f32(sr_biases[ch >> 1]) * xs;
+    }
+    d = wave_sum(d);
+    if (lane == 0) part[wave] = d;
+    __syncthreads();
+    const float gate = sigmoidf_((part[0] + part[1]) + (part[2] + part[3]));
+    float p[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) p[s] = probs[(size_t)t * 8 + s];
+    const float *sh = route_out + ((size_t)tokens * 8 + t) * H;
+    const float *ro = route_out + (size_t)t * 8 * H;
+    for (int c = tid; c < H; c += 256) {
+        float y = sh[c] * gate;
+#pragma unroll
+        for (int s = 0; s < 8; s++) y += ro[(size_t)s * H + c] * p[s];
+        const size_t at = (size_t)t * H + c;
+        residual[at] = f32_to_bf16(bf16_to_f32(residual[at]) + y);
+    }
+}
+
+bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens, int hidden,
+                      const float *route_out, const float *probs, uint16_t *residual,
+                      hipStream_t s, char *error, int capacity) {
+    if (shared_route->bits == 8)
+        hipLaunchKernelGGL((merge_kernel<8>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
+                           shared_route->scales(), shared_route->biases(), x, tokens, hidden, route_out,
+                           probs, residual);
+    else
+        hipLaunchKernelGGL((merge_kernel<5>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
+                           shared_route->scales(), shared_route->biases(), x, tokens, hidden, route_out,
+                           probs, residual);
+    return hip_ok(hipGetLastError(), error, capacity, "merge launch");
+}
+
+// --------------------------------------------------------------------------- argmax
+
+// Two levels in one launch (graph_argmax_blocks/final gpu_graph.mm:160-175): each block
+// reduces 1024 values to (max, lowest index), flagging non-finite values; the last block
+// to finish reduces the partials. Result 0xffffffff when any value is not finite.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *v, int n, float *pval,
+                                                     uint32_t *pidx, uint32_t *ticket,
+                                                     uint32_t *next) {
+    __shared__ float wv[4];
+    __shared__ uint32_t wi[4];
+    __shared__ int last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float best = -INFINITY;
+    uint32_t id = 0xffffffffu;
+    bool bad = false;
+    const int base = blockIdx.x * 1024;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int at = base + k * 256 + tid;
+        if (at < n) {
+            const float x = v[at];
+            if (!isfinite(x)) bad = true;
+            else if (x > best || (x == best && (uint32_t)at < id)) { best = x; id = (uint32_t)at; }
+        }
+    }
+    const bool any_bad_w = __any(bad);
+    float m = wave_max(best);
+    uint32_t sel = wave_min_u32(best == m ? id : 0xffffffffu);
+    if (lane == 0) { wv[wave] = m; wi[wave] = any_bad_w ? 0xfffffffeu : sel; }
+    __syncthreads();
+    if (tid == 0) {
+        float bm = wv[0];
+        uint32_t bi = wi[0];
+        bool invalid = wi[0] == 0xfffffffeu;
+        for (int w = 1; w < 4; w++) {
+            if (wi[w] == 0xfffffffeu) { invalid = true; continue; }
+            if (wv[w] > bm || (wv[w] == bm && wi[w] < bi) || bi == 0xfffffffeu) { bm = wv[w]; bi = wi[w]; }
+        }
+        pval[blockIdx.x] = bm;
+        pidx[blockIdx.x] = invalid ? 0xfffffffeu : bi;
+        __threadfence();
+        last = (atomicAdd(ticket, 1u) == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float b2 = -INFINITY;
+    uint32_t i2 = 0xffffffffu;
+    bool bad2 = false;
+    for (int k = tid; k < (int)gridDim.x; k += 256) {
+        const uint32_t pi = pidx[k];
+        const float pv = pval[k];
+        if (pi == 0xfffffffeu) bad2 = true;
+        else if (pi != 0xffffffffu && (pv > b2 || (pv == b2 && pi < i2))) { b2 = pv; i2 = pi; }
+    }
+    const bool bad_w = __any(bad2);
+    float m2 = wave_max(b2);
+    uint32_t s2 = wave_min_u32(b2 == m2 ? i2 : 0xffffffffu);
+    if (lane == 0) { wv[wave] = m2; wi[wave] = bad_w ? 0xfffffffeu : s2; }
+    __syncthreads();
+    if (tid == 0) {
+        float bm = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        bool invalid = false;
+        for (int w = 0; w < 4; w++) {
+            if (wi[w] == 0xfffffffeu) { invalid = true; continue; }
+            if (wi[w] != 0xffffffffu && (wv[w] > bm || (wv[w] == bm && wi[w] < bi))) { bm = wv[w]; bi = wi[w]; }
+        }
+        *next = invalid ? 0xffffffffu : bi;
+        *ticket = 0u;
+    }
+}
+
+bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
+                   uint32_t *ticket, uint32_t *next, hipStream_t s, char *error, int capacity) {
+    const int blocks = (n + 1023) / 1024;
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, values, n, part_val, part_idx,
+                       ticket, next);
+    return hip_ok(hipGetLastError(), error, capacity, "argmax launch");
+}
+
+}  // namespace dih

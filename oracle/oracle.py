@@ -1,0 +1,284 @@
+"""Python side of the CPU oracle (test infrastructure only).
+
+Loads ``liboracle.so`` (built from oracle.c by ``make -C oracle``) and adds numpy helpers
+that the tests use to build MLX-affine matrices. Only tests/, ``__graft_entry__.smoke()``
+and bench.py's ``cpu_baseline`` leg import this module; the product never does.
+
+Layout restated from the reference's loader and packers:
+  packed uint32 [E, R, C*bits/32], code c at bit c*bits LSB-first, straddling words
+  (Qwen36Weights.cs:73-76; QuantizedTests.cs:155-161), scales/biases bf16 [E, R, C/64].
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class OrcMatrix(ctypes.Structure):
+    _fields_ = [("packed", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("biases", ctypes.c_void_p), ("experts", ctypes.c_int),
+                ("rows", ctypes.c_int), ("columns", ctypes.c_int), ("bits", ctypes.c_int)]
+
+
+class OrcMoeLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.POINTER(OrcMatrix)) for n in
+                ("router", "gate", "up", "down", "shared_gate", "shared_up",
+                 "shared_down", "shared_route")]
+
+
+def _declare(L):
+    P = ctypes.c_void_p
+    I = ctypes.c_int
+    M = ctypes.POINTER(OrcMatrix)
+    L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_bf16_to_f32.restype = ctypes.c_float
+    L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+    L.orc_f32_to_bf16.restype = ctypes.c_uint16
+    L.orc_code.argtypes = [P, I, I]
+    L.orc_code.restype = ctypes.c_uint32
+    L.orc_dequant_row.argtypes = [M, I, I, P]
+    L.orc_qmv_f64.argtypes = [M, P, P, I, I, P]
+    L.orc_dense_f64.argtypes = [M, I, P, I, I, P]
+    L.orc_top8.argtypes = [P, I, P, P]
+    L.orc_top8.restype = I
+    L.orc_top8_bf16.argtypes = [P, I, I, P, P]
+    L.orc_top8_bf16.restype = I
+    L.orc_build_groups.argtypes = [P, I, I, P, P]
+    L.orc_argmax.argtypes = [P, I]
+    L.orc_argmax.restype = ctypes.c_uint32
+    L.orc_expert_mlp_f64.argtypes = [M, M, M, M, P, P, P, I, P, P]
+    L.orc_moe_f64.argtypes = [ctypes.POINTER(OrcMoeLayer), I, P, P, P, I, P, P]
+    L.orc_cpu_qmv.argtypes = [M, P, P, I, I, P, I]
+    L.orc_cpu_moe_token.argtypes = [ctypes.POINTER(OrcMoeLayer), P, P, I]
+    L.orc_cpu_moe_token.restype = I
+    L.orc_openmp_threads.restype = I
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- bf16 helpers (numpy)
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(f: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even (the rule of prefill_expert_checks.mm:24)."""
+    u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFFFFFF
+    return (u >> 16).astype(np.uint16)
+
+
+def round_bf16(f: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(f))
+
+
+# ---------------------------------------------------------------- packing (numpy)
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Pack integer codes [..., C] LSB-first at bit c*bits into uint32 words
+    (the packer of QuantizedTests.cs:155-161 / prefill_expert_checks.mm:16-17)."""
+    codes = np.asarray(codes, dtype=np.uint64)
+    *lead, C = codes.shape
+    assert (C * bits) % 32 == 0
+    words = np.zeros(lead + [C * bits // 32], dtype=np.uint64)
+    for c in range(C):
+        bit = c * bits
+        at, shift = bit // 32, bit % 32
+        words[..., at] |= (codes[..., c] << shift) & 0xFFFFFFFF
+        if shift + bits > 32:
+            words[..., at + 1] |= codes[..., c] >> (32 - shift)
+    return words.astype(np.uint32)
+
+
+def unpack_codes(words: np.ndarray, bits: int, columns: int) -> np.ndarray:
+    """Independent numpy unpack: treat each row as one little-endian bit string."""
+    w = np.ascontiguousarray(words, dtype=np.uint32)
+    *lead, nw = w.shape
+    bitsarr = np.unpackbits(w.view(np.uint8).reshape(*lead, nw * 4), axis=-1, bitorder="little")
+    bitsarr = bitsarr[..., : columns * bits].reshape(*lead, columns, bits).astype(np.uint32)
+    return (bitsarr << np.arange(bits, dtype=np.uint32)).sum(axis=-1).astype(np.uint32)
+
+
+class QMatrix:
+    """A host MLX-affine matrix plus its ctypes view for the C oracle."""
+
+    def __init__(self, packed, scales, biases, experts, rows, columns, bits):
+        self.packed = np.ascontiguousarray(packed, dtype=np.uint32)
+        self.scales = np.ascontiguousarray(scales, dtype=np.uint16)
+        self.biases = np.ascontiguousarray(biases, dtype=np.uint16)
+        self.experts, self.rows, self.columns, self.bits = experts, rows, columns, bits
+        assert self.packed.size == experts * rows * columns * bits // 32
+        assert self.scales.size == experts * rows * columns // 64 == self.biases.size
+        self.c = OrcMatrix(self.packed.ctypes.data, self.scales.ctypes.data,
+                           self.biases.ctypes.data, experts, rows, columns, bits)
+
+    @classmethod
+    def from_codes(cls, codes, scales, biases, bits):
+        E, R, C = codes.shape
+        return cls(pack_codes(codes, bits), scales, biases, E, R, C, bits)
+
+    def dequant(self, round_bf=False) -> np.ndarray:
+        """Dense float32 weights [E, R, C] (numpy, independent of oracle.c)."""
+        codes = unpack_codes(self.packed.reshape(self.experts, self.rows, -1), self.bits, self.columns)
+        s = bf16_bits_to_f32(self.scales).reshape(self.experts, self.rows, -1)
+        b = bf16_bits_to_f32(self.biases).reshape(self.experts, self.rows, -1)
+        s = np.repeat(s, 64, axis=-1)
+        b = np.repeat(b, 64, axis=-1)
+        w = (codes.astype(np.float32) * s + b).astype(np.float32)
+        return round_bf16(w) if round_bf else w
+
+
+def random_matrix(rng: np.random.Generator, experts, rows, columns, bits, scale_lo=5e-4,
+                  scale_hi=2e-3, bias_sd=1e-4) -> QMatrix:
+    """Synthetic MLX-affine weights of the benchmark configs: codes U{0..2^bits-1} (uniform
+    random packed words, so every bit field is uniform), scale ~U(lo, hi) in bf16,
+    bias = -2^(bits-1)*scale + N(0, bias_sd) in bf16."""
+    words = rng.integers(0, 1 << 32, size=(experts, rows, columns * bits // 32), dtype=np.uint64)
+    s = rng.uniform(scale_lo, scale_hi, size=(experts, rows, columns // 64)).astype(np.float32)
+    sb = f32_to_bf16_bits(s)
+    b = -(1 << (bits - 1)) * bf16_bits_to_f32(sb) + rng.normal(0, bias_sd, size=s.shape).astype(np.float32)
+    return QMatrix(words.astype(np.uint32), sb, f32_to_bf16_bits(b.astype(np.float32)), experts, rows,
+                   columns, bits)
+
+
+# ---------------------------------------------------------------- oracle wrappers
+
+def qmv_f64(m: QMatrix, x: np.ndarray, experts=None, batched=False) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    count = 1 if experts is None else len(experts)
+    ids = None if experts is None else np.ascontiguousarray(experts, dtype=np.uint32)
+    y = np.zeros(count * m.rows, dtype=np.float64)
+    lib().orc_qmv_f64(ctypes.byref(m.c), _ptr(x), None if ids is None else _ptr(ids), count,
+                      1 if batched else 0, _ptr(y))
+    return y
+
+
+def dense_f64(m: QMatrix, x: np.ndarray, expert=0, round_operands=True) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.zeros((T, m.rows), dtype=np.float64)
+    lib().orc_dense_f64(ctypes.byref(m.c), expert, _ptr(x), T, 1 if round_operands else 0, _ptr(y))
+    return y
+
+
+def top8(logits: np.ndarray):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.zeros(8, dtype=np.int32)
+    probs = np.zeros(8, dtype=np.float32)
+    rc = lib().orc_top8(_ptr(logits), logits.size, _ptr(ids), _ptr(probs))
+    if rc != 0:
+        raise ValueError("Non-finite router logits.")
+    return ids, probs
+
+
+def top8_bf16(logits_bits: np.ndarray):
+    logits_bits = np.ascontiguousarray(logits_bits, dtype=np.uint16)
+    T, E = logits_bits.shape
+    ids = np.zeros((T, 8), dtype=np.int32)
+    probs = np.zeros((T, 8), dtype=np.float32)
+    bad = lib().orc_top8_bf16(_ptr(logits_bits), T, E, _ptr(ids), _ptr(probs))
+    if bad >= 0:
+        raise ValueError(f"Non-finite router logits at token {bad}.")
+    return ids, probs
+
+
+def build_groups(ids: np.ndarray, tokens: int, experts: int):
+    ids = np.ascontiguousarray(ids, dtype=np.uint32).reshape(-1)
+    counts = np.zeros(experts, dtype=np.uint32)
+    routes = np.zeros(experts * tokens, dtype=np.uint32)
+    lib().orc_build_groups(_ptr(ids), tokens, experts, _ptr(counts), _ptr(routes))
+    return counts, routes
+
+
+def argmax(values: np.ndarray) -> int:
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    return int(lib().orc_argmax(_ptr(values), values.size))
+
+
+def expert_mlp_f64(gate, up, down, shared, x, sx, experts):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    sx = np.ascontiguousarray(sx, dtype=np.float32)
+    ids = np.ascontiguousarray(experts, dtype=np.uint32)
+    out = np.zeros(len(ids) * down.rows, dtype=np.float64)
+    sout = np.zeros(shared.rows, dtype=np.float64)
+    lib().orc_expert_mlp_f64(ctypes.byref(gate.c), ctypes.byref(up.c), ctypes.byref(down.c),
+                             ctypes.byref(shared.c), _ptr(x), _ptr(sx), _ptr(ids), len(ids),
+                             _ptr(out), _ptr(sout))
+    return out, sout
+
+
+class MoeLayer:
+    """Host weights of one MoE layer (Qwen36Weights.cs:93-100)."""
+
+    def __init__(self, router, gate, up, down, shared_gate, shared_up, shared_down, shared_route):
+        self.router, self.gate, self.up, self.down = router, gate, up, down
+        self.shared_gate, self.shared_up = shared_gate, shared_up
+        self.shared_down, self.shared_route = shared_down, shared_route
+        P = ctypes.pointer
+        self.c = OrcMoeLayer(*(P(m.c) if m is not None else ctypes.POINTER(OrcMatrix)()
+                               for m in (router, gate, up, down, shared_gate, shared_up,
+                                         shared_down, shared_route)))
+
+
+def moe_f64(layer: MoeLayer, x: np.ndarray, ids: np.ndarray, probs: np.ndarray,
+            bf16_operands=True, route_out=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H = x.shape
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    probs = np.ascontiguousarray(probs, dtype=np.float32)
+    y = np.zeros((T, H), dtype=np.float64)
+    ro = np.zeros((T * 9, H), dtype=np.float64) if route_out else None
+    lib().orc_moe_f64(ctypes.byref(layer.c), T, _ptr(x), _ptr(ids), _ptr(probs),
+                      1 if bf16_operands else 0, _ptr(y), None if ro is None else _ptr(ro))
+    return (y, ro) if route_out else y
+
+
+def cpu_qmv(m: QMatrix, x, experts=None, batched=False, threads=1) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    count = 1 if experts is None else len(experts)
+    ids = None if experts is None else np.ascontiguousarray(experts, dtype=np.uint32)
+    y = np.zeros(count * m.rows, dtype=np.float32)
+    lib().orc_cpu_qmv(ctypes.byref(m.c), _ptr(x), None if ids is None else _ptr(ids), count,
+                      1 if batched else 0, _ptr(y), threads)
+    return y
+
+
+def cpu_moe_token(layer: MoeLayer, x, threads=1) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros(layer.down.rows, dtype=np.float32)
+    if lib().orc_cpu_moe_token(ctypes.byref(layer.c), _ptr(x), _ptr(y), threads) != 0:
+        raise ValueError("Non-finite router logits.")
+    return y
+
+
+def rel_err(actual, expected) -> float:
+    """max |actual - expected| / RMS(expected): the north-star tolerance measure."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(e * e)))
+    return float(np.max(np.abs(a - e))) / max(rms, 1e-30)

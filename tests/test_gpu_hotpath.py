@@ -1,0 +1,418 @@
+"""GPU parity tests of the device-resident hot path against the CPU oracle.
+
+Integer work (top-8 ids, grouping, argmax, bf16 dequantization) must be bit-exact.
+Matmul outputs must satisfy max|gpu - oracle| / RMS(oracle) <= TOL (1e-2, the north-star
+tolerance) against the fp64 oracle of the reference's dequantize-then-matmul; tighter
+bounds are asserted where the arithmetic allows (noted per test).
+"""
+import numpy as np
+import pytest
+import torch
+
+import deepinfer_hip as dh
+from oracle import oracle as orc
+from tests import refcases
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def upload(device, host: orc.QMatrix):
+    m = device.allocate(host.experts, host.rows, host.columns, host.bits)
+    m.upload(0, host.packed)
+    m.upload(1, host.scales)
+    m.upload(2, host.biases)
+    return m
+
+
+def dev_bf16(bits_u16: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits_u16, dtype=np.uint16).view(np.int16)).cuda()
+
+
+def host_bf16(t: torch.Tensor) -> np.ndarray:
+    return orc.bf16_bits_to_f32(t.cpu().numpy().view(np.uint16))
+
+
+def u32(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint32)
+
+
+def assert_rounded(got, exact, err_scale):
+    """A bf16 result must equal a value within TOL*err_scale of the fp64 answer, rounded to
+    bf16: |got - exact| <= 2^-8*|exact| (one round-to-nearest-even step) + TOL*err_scale."""
+    got = np.asarray(got, dtype=np.float64)
+    exact = np.asarray(exact, dtype=np.float64)
+    bound = np.abs(exact) * 2.0 ** -8 + TOL * err_scale
+    worst = np.max(np.abs(got - exact) - bound)
+    assert worst <= 0, worst
+
+
+def rms(a) -> float:
+    a = np.asarray(a, dtype=np.float64)
+    return float(np.sqrt(np.mean(a * a)))
+
+
+# ------------------------------------------------------------------------------ qmv
+
+@pytest.mark.parametrize("bits,rows,columns", [(8, 4096, 2048), (5, 4096, 2048), (8, 300, 512),
+                                               (5, 129, 4096), (8, 97, 192), (5, 64, 64)])
+def test_qmv_bf16_matches_fp64_oracle(device, bits, rows, columns):
+    """Config-1 shape (8-bit [4096x2048], x bf16 ~N(0,1), bf16 out) and tails/odd widths."""
+    rng = np.random.default_rng(0)
+    host = orc.random_matrix(rng, 1, rows, columns, bits)
+    m = upload(device, host)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=columns).astype(np.float32))
+        x = dev_bf16(xb)
+        want = orc.qmv_f64(host, orc.bf16_bits_to_f32(xb))
+        y32 = torch.zeros(rows, dtype=torch.float32, device="cuda")
+        yb = torch.zeros(rows, dtype=torch.int16, device="cuda")
+        dh.qmv(device, m, x, y32, y_dtype=dh.F32)
+        dh.qmv(device, m, x, yb, y_dtype=dh.BF16)
+        torch.cuda.synchronize()
+        e32 = orc.rel_err(y32.cpu().numpy(), want)
+        assert e32 < TOL and e32 < 1e-5, e32          # fp32 accumulation only
+        # the bf16 output is the RNE rounding of that f32 result ...
+        assert np.array_equal(yb.cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(y32.cpu().numpy()))
+        # ... hence within one bf16 rounding step of the fp64 answer
+        assert_rounded(host_bf16(yb), want, rms(want))
+    finally:
+        m.dispose()
+
+
+def test_qmv_experts_batched_and_bad_ids(device):
+    rng = np.random.default_rng(1)
+    host = orc.random_matrix(rng, 9, 129, 512, 8)
+    m = upload(device, host)
+    try:
+        ids = np.array([8, 0, 6, 2, 5, 1, 7, 3], dtype=np.uint32)
+        x = rng.normal(size=8 * 512).astype(np.float32)
+        y = torch.zeros(8 * 129, dtype=torch.float32, device="cuda")
+        dh.qmv(device, m, torch.from_numpy(x).cuda(), y, experts=torch.from_numpy(ids.view(np.int32)).cuda(),
+               count=8, batched=True, x_dtype=dh.F32)
+        torch.cuda.synchronize()
+        want = orc.qmv_f64(host, x, ids, batched=True)
+        assert orc.rel_err(y.cpu().numpy(), want) < 1e-5
+        bad = torch.tensor([3, 9], dtype=torch.int32, device="cuda")
+        y2 = torch.zeros(2 * 129, dtype=torch.float32, device="cuda")
+        dh.qmv(device, m, torch.from_numpy(x).cuda(), y2, experts=bad, count=2, batched=True, x_dtype=dh.F32)
+        torch.cuda.synchronize()
+        out = y2.cpu().numpy()
+        assert np.all(np.isfinite(out[:129])) and np.all(np.isnan(out[129:]))
+    finally:
+        m.dispose()
+
+
+def test_dequant_bf16_is_bit_exact(device):
+    """expanded_weights semantics: bf16 RNE of fp32(q*scale+bias), both bit widths."""
+    rng = np.random.default_rng(2)
+    for bits in (5, 8):
+        host = orc.random_matrix(rng, 3, 77, 320, bits)
+        m = upload(device, host)
+        try:
+            out = torch.zeros((77, 320), dtype=torch.int16, device="cuda")
+            dh.dequant_bf16(device, m, 2, out)
+            torch.cuda.synchronize()
+            want = orc.f32_to_bf16_bits(host.dequant()[2])
+            assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+        finally:
+            m.dispose()
+
+
+# --------------------------------------------------------------------------- routing
+
+def test_top8_known_answers(device):
+    """graph_checks.mm:63-77 cases plus the routing KAT of QuantizedTests.cs:280-288."""
+    cases = refcases.top8_cases()
+    logits = torch.from_numpy(np.stack(cases)).cuda()
+    ids = torch.zeros((5, 8), dtype=torch.int32, device="cuda")
+    probs = torch.zeros((5, 8), dtype=torch.float32, device="cuda")
+    dh.top8(device, logits, 5, 256, ids, probs, logits_dtype=dh.F32)
+    torch.cuda.synchronize()
+    for k, v in enumerate(cases):
+        exp = refcases.stable_top8(v)
+        assert np.array_equal(ids.cpu().numpy()[k], exp), k
+        chosen = v[exp].astype(np.float64)
+        p = np.exp(chosen - chosen[0])
+        p /= p.sum()
+        assert np.max(np.abs(probs.cpu().numpy()[k] - p)) <= 1e-6
+    assert list(ids.cpu().numpy()[1]) == list(range(255, 247, -1))
+    assert abs(probs.cpu().numpy()[1].sum() - 1) <= 1e-6
+
+
+def test_top8_bf16_random_with_ties_matches_oracle(device):
+    rng = np.random.default_rng(3)
+    T = 2048
+    lg = rng.normal(size=(T, 256)).astype(np.float32)
+    lg[::7, 10:40] = 2.5          # many exact ties among the top values
+    lb = orc.f32_to_bf16_bits(lg)
+    ids = torch.zeros((T, 8), dtype=torch.int32, device="cuda")
+    probs = torch.zeros((T, 8), dtype=torch.float32, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    dh.top8(device, dev_bf16(lb), T, 256, ids, probs, status=status)
+    torch.cuda.synchronize()
+    oid, opr = orc.top8_bf16(lb)
+    assert np.array_equal(ids.cpu().numpy(), oid)
+    assert np.max(np.abs(probs.cpu().numpy() - opr)) <= 1e-6
+    assert int(status.item()) == 0
+
+
+def test_top8_flags_non_finite(device):
+    lg = np.zeros((2, 256), dtype=np.float32)
+    lg[1, 17] = np.nan
+    ids = torch.zeros((2, 8), dtype=torch.int32, device="cuda")
+    probs = torch.zeros((2, 8), dtype=torch.float32, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    dh.top8(device, torch.from_numpy(lg).cuda(), 2, 256, ids, probs, status=status, logits_dtype=dh.F32)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1
+    assert list(ids.cpu().numpy()[0]) == list(range(8))
+
+
+@pytest.mark.parametrize("count", [64, 65, 127, 128, 129, 512, 513, 2048])
+@pytest.mark.parametrize("pattern", [0, 1, 2])
+def test_build_groups_is_bit_exact(device, count, pattern):
+    """Route lists, counts and their invariants (prefill_expert_checks.mm:26-52)."""
+    ids = refcases.route_pattern(pattern, count)
+    counts = torch.zeros(256, dtype=torch.int32, device="cuda")
+    routes = torch.zeros(256 * count, dtype=torch.int32, device="cuda")
+    dh.build_groups(device, torch.from_numpy(ids.view(np.int32)).cuda(), count, 256, counts, routes)
+    torch.cuda.synchronize()
+    oc, orr = orc.build_groups(ids, count, 256)
+    gc, gr = u32(counts), u32(routes)
+    assert np.array_equal(gc, oc)
+    seen = np.zeros(count * 8, dtype=bool)
+    flat = ids.reshape(-1)
+    for e in range(256):
+        lst = gr[e * count:e * count + gc[e]]
+        assert np.array_equal(lst, orr[e * count:e * count + oc[e]])
+        assert np.all(np.diff(lst.astype(np.int64)) > 0)
+        assert np.all(flat[lst] == e)
+        assert not seen[lst].any()
+        seen[lst] = True
+    assert seen.all()
+
+
+# --------------------------------------------------------------------------- lm_head
+
+def _lm_slices(device, rng, rows_per_slice, columns, n=4):
+    hosts = [orc.random_matrix(rng, 1, rows_per_slice, columns, 8) for _ in range(n)]
+    return hosts, [upload(device, h) for h in hosts]
+
+
+def test_lm_head_split_logits_and_argmax(device):
+    rng = np.random.default_rng(4)
+    hosts, slices = _lm_slices(device, rng, 6208, 2048)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=2048).astype(np.float32))
+        logits = torch.zeros(4 * 6208, dtype=torch.float32, device="cuda")
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        dh.lm_head(device, slices, dev_bf16(xb), logits, nxt)
+        torch.cuda.synchronize()
+        xf = orc.bf16_bits_to_f32(xb)
+        want = np.concatenate([orc.qmv_f64(h, xf) for h in hosts])
+        got = logits.cpu().numpy()
+        assert orc.rel_err(got, want) < 1e-5
+        assert int(u32(nxt)[0]) == orc.argmax(got)
+    finally:
+        for s in slices:
+            s.dispose()
+
+
+def test_argmax_known_answers(device):
+    """graph_checks.mm:89-103 and ModelTests.cs:23-28."""
+    n = 248320
+    base = (np.arange(n, dtype=np.float32) * np.float32(1e-5)).astype(np.float32)
+    cases = []
+    cases.append((base.copy(), 248319))
+    t = base.copy(); t[100] = t[200] = 10; cases.append((t, 100))
+    t = base.copy(); t[0] = np.nan; cases.append((t, 0xFFFFFFFF))
+    t = base.copy(); t[5000] = np.inf; cases.append((t, 0xFFFFFFFF))
+    cases.append((np.array([1, 3, 3], dtype=np.float32), 1))
+    t = np.full(5000, -7, dtype=np.float32); t[1023] = t[1024] = t[4999] = -1; cases.append((t, 1023))
+    for v, want in cases:
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        dh.argmax(device, torch.from_numpy(v).cuda(), v.size, nxt)
+        torch.cuda.synchronize()
+        assert int(u32(nxt)[0]) == want
+        assert orc.argmax(v) == want
+
+
+# ------------------------------------------------------------------------------- MoE
+
+def _moe_layer(rng, E, H, I, bits, router=True):
+    mk = lambda e, r, c, b=bits: orc.random_matrix(rng, e, r, c, b)  # noqa: E731
+    rt = orc.random_matrix(rng, 1, E, H, 8, scale_lo=1.25e-4, scale_hi=5e-4) if router else None
+    return orc.MoeLayer(rt, mk(E, I, H), mk(E, I, H), mk(E, H, I), mk(1, I, H), mk(1, I, H), mk(1, H, I),
+                        orc.random_matrix(rng, 1, 1, H, 8))
+
+
+def _upload_layer(device, L):
+    mats = [L.router, L.gate, L.up, L.down, L.shared_gate, L.shared_up, L.shared_down, L.shared_route]
+    q = [None if m is None else upload(device, m) for m in mats]
+    return q, dh.make_layer(*q)
+
+
+@pytest.mark.parametrize("bits", [8, 5])
+def test_moe_decode_step_matches_oracle(device, bits):
+    """Decode MoE step (config 2 shapes with 8-bit; 5-bit experts with 8-bit router)."""
+    rng = np.random.default_rng(5)
+    E, H, I = 256, 2048, 512
+    L = _moe_layer(rng, E, H, I, bits)
+    q, layer = _upload_layer(device, L)
+    try:
+        for step in range(3):
+            xb = orc.f32_to_bf16_bits(rng.normal(size=H).astype(np.float32))
+            rb = orc.f32_to_bf16_bits((rng.normal(size=H) * (0 if step == 0 else 1)).astype(np.float32))
+            res = dev_bf16(rb)
+            lg = torch.zeros(E, dtype=torch.float32, device="cuda")
+            ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+            probs = torch.zeros(8, dtype=torch.float32, device="cuda")
+            status = torch.zeros(1, dtype=torch.int32, device="cuda")
+            rout = torch.zeros((9, H), dtype=torch.float32, device="cuda")
+            dh.moe_decode(device, layer, dev_bf16(xb), res,
+                          trace=dh.make_trace(logits=lg, ids=ids, probs=probs, status=status, expert_out=rout))
+            torch.cuda.synchronize()
+            xf = orc.bf16_bits_to_f32(xb)
+            # router logits: fp32 GEMV vs fp64
+            want_lg = orc.qmv_f64(L.router, xf)
+            got_lg = lg.cpu().numpy()
+            assert orc.rel_err(got_lg, want_lg) < 1e-5
+            # routing decided on the GPU's logits must be bit-exact with the oracle's rule
+            oid, opr = orc.top8(got_lg)
+            assert np.array_equal(ids.cpu().numpy(), oid)
+            assert np.max(np.abs(probs.cpu().numpy() - opr)) <= 1e-6
+            y, ro = orc.moe_f64(L, xf[None, :], oid[None, :], opr[None, :], bf16_operands=False, route_out=True)
+            # matmul outputs (8 slot down projections + shared down): fp32 GEMVs vs fp64
+            err = orc.rel_err(rout.cpu().numpy(), ro)
+            assert err < TOL and err < 1e-4, err
+            # residual = bf16(residual + y)
+            assert_rounded(host_bf16(res), orc.bf16_bits_to_f32(rb) + y[0], rms(y))
+            assert int(status.item()) == 0
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
+def test_moe_decode_with_supplied_logits(device):
+    rng = np.random.default_rng(6)
+    E, H, I = 64, 512, 256
+    L = _moe_layer(rng, E, H, I, 8, router=False)
+    q, layer = _upload_layer(device, L)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=H).astype(np.float32))
+        lg = rng.normal(size=E).astype(np.float32)
+        res = torch.zeros(H, dtype=torch.int16, device="cuda")
+        ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+        dh.moe_decode(device, layer, dev_bf16(xb), res, logits=torch.from_numpy(lg).cuda(),
+                      trace=dh.make_trace(ids=ids))
+        torch.cuda.synchronize()
+        oid, opr = orc.top8(lg)
+        assert np.array_equal(ids.cpu().numpy(), oid)
+        y = orc.moe_f64(L, orc.bf16_bits_to_f32(xb)[None, :], oid[None, :], opr[None, :], bf16_operands=False)[0]
+        assert_rounded(host_bf16(res), y, rms(y))
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
+def _zipf_logits(rng, T, E, s=1.1):
+    """Router logits log p_e + Gumbel with p ~ rank^-s: top-8 = Zipf sampling without
+    replacement (config 3)."""
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    perm = rng.permutation(E)
+    g = rng.gumbel(size=(T, E))
+    return (np.log(p)[perm][None, :] + g).astype(np.float32)
+
+
+@pytest.mark.parametrize("T,E,H,I,bits,routing", [
+    (64, 32, 256, 128, 8, "zipf"), (65, 32, 256, 128, 5, "uniform"), (200, 256, 512, 128, 8, "zipf"),
+    (129, 16, 128, 192, 5, "uniform"), (1, 16, 128, 64, 8, "uniform")])
+def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
+    rng = np.random.default_rng(T * 7 + E)
+    L = _moe_layer(rng, E, H, I, bits, router=False)
+    q, layer = _upload_layer(device, L)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+        lg = _zipf_logits(rng, T, E) if routing == "zipf" else rng.normal(size=(T, E)).astype(np.float32)
+        lb = orc.f32_to_bf16_bits(lg)
+        rb = orc.f32_to_bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+        res = dev_bf16(rb)
+        ids = torch.zeros((T, 8), dtype=torch.int32, device="cuda")
+        probs = torch.zeros((T, 8), dtype=torch.float32, device="cuda")
+        rout = torch.zeros((T * 9, H), dtype=torch.float32, device="cuda")
+        dh.moe_prefill(device, layer, T, dev_bf16(xb), dev_bf16(lb), res,
+                       trace=dh.make_trace(ids=ids, probs=probs, expert_out=rout))
+        torch.cuda.synchronize()
+        oid, opr = orc.top8_bf16(lb)
+        assert np.array_equal(ids.cpu().numpy(), oid)
+        assert np.max(np.abs(probs.cpu().numpy() - opr)) <= 1e-6
+        xf = orc.bf16_bits_to_f32(xb)
+        got_ro = rout.cpu().numpy()
+        # per-route down outputs against the oracle with the reference's bf16 operand
+        # rounding (weights, x, SwiGLU activation) and against the unrounded fp64 oracle
+        _, ro_bf = orc.moe_f64(L, xf, oid, opr, bf16_operands=True, route_out=True)
+        y, ro = orc.moe_f64(L, xf, oid, opr, bf16_operands=False, route_out=True)
+        e_bf, e_exact = orc.rel_err(got_ro, ro_bf), orc.rel_err(got_ro, ro)
+        assert e_bf < TOL and e_exact < TOL, (e_bf, e_exact)
+        # residual = bf16(residual + sigmoid-gated shared + probability-weighted experts)
+        assert_rounded(host_bf16(res), orc.bf16_bits_to_f32(rb).astype(np.float64) + y, rms(y))
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
+@pytest.mark.parametrize("bits,rows,columns,T", [(8, 512, 2048, 256), (5, 300, 512, 130), (8, 129, 256, 65),
+                                                 (8, 2048, 4096, 64)])
+def test_dense_matches_oracle(device, bits, rows, columns, T):
+    rng = np.random.default_rng(rows + T)
+    host = orc.random_matrix(rng, 1, rows, columns, bits)
+    m = upload(device, host)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, columns)).astype(np.float32))
+        y = torch.zeros((T, rows), dtype=torch.float32, device="cuda")
+        dh.dense(device, m, T, dev_bf16(xb), y)
+        torch.cuda.synchronize()
+        xf = orc.bf16_bits_to_f32(xb)
+        want_bf = orc.dense_f64(host, xf, round_operands=True)
+        assert orc.rel_err(y.cpu().numpy(), want_bf) < 1e-4
+        want = orc.dense_f64(host, xf, round_operands=False)
+        assert orc.rel_err(y.cpu().numpy(), want) < TOL
+    finally:
+        m.dispose()
+
+
+def test_bf16_dense_check_cases(device):
+    """bf16_checks.mm:12-35: closed-form weights, amplitudes .2 and 1e10, relative L2 < 2e-5
+    against bf16-rounded double products."""
+    cols = 256
+    for rows in (32, 129):
+        for bits in (5, 8):
+            r = np.arange(rows)[:, None]
+            g = np.arange(4)[None, :]
+            scale = orc.round_bf16((np.float32(.00017) * (1 + (r + g) % 13)).astype(np.float32))
+            bias = orc.round_bf16((np.float32(-.0271) * (1 + (r + g) % 3)).astype(np.float32))
+            c = np.arange(cols)[None, :]
+            q = ((r * 37 + c * 19 + 7) & ((1 << bits) - 1)).astype(np.uint32)
+            host = orc.QMatrix(orc.pack_codes(q[None], bits), orc.f32_to_bf16_bits(scale),
+                               orc.f32_to_bf16_bits(bias), 1, rows, cols, bits)
+            m = upload(device, host)
+            try:
+                for n in (64, 65, 128, 2048):
+                    for amp in (.2, 1e10):
+                        i = np.arange(n * cols)
+                        x = (np.sin(i * np.float32(.019)).astype(np.float32) * np.float32(amp)).reshape(n, cols)
+                        xb = orc.f32_to_bf16_bits(x)
+                        y = torch.zeros((n, rows), dtype=torch.float32, device="cuda")
+                        dh.dense(device, m, n, dev_bf16(xb), y)
+                        torch.cuda.synchronize()
+                        want = orc.dense_f64(host, orc.bf16_bits_to_f32(xb), round_operands=True)
+                        got = y.cpu().numpy().astype(np.float64)
+                        rel = np.sqrt(((got - want) ** 2).sum() / max((want ** 2).sum(), 1e-30))
+                        assert rel < 2e-5, (rows, bits, n, amp, rel)
+            finally:
+                m.dispose()

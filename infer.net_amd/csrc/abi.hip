@@ -54,35 +54,44 @@ bool sync_matrix(Matrix *m, char *error, int capacity) {
     return true;
 }
 
-static int prof_event(Context *c, hipStream_t s) {
+static thread_local Context *tl_prof_ctx = nullptr;
+static thread_local const char *tl_prof_name = "kernel";
+static thread_local size_t tl_prof_first = 0;  // first record not yet named by prof_mark
+
+ProfScope::ProfScope(Context *c) {
+    tl_prof_ctx = c && c->profiling ? c : nullptr;
+    tl_prof_name = "kernel";
+    tl_prof_first = tl_prof_ctx ? tl_prof_ctx->prof_recs.size() : 0;
+}
+ProfScope::~ProfScope() { tl_prof_ctx = nullptr; }
+void prof_stage(const char *name) { tl_prof_name = name; }
+
+// Names the launches recorded since the previous mark (the kernels of one stage).
+static void prof_mark(Context *c, hipStream_t, const char *name) {
+    if (!c->profiling || tl_prof_ctx != c) return;
+    for (size_t i = tl_prof_first; i < c->prof_recs.size(); i++) c->prof_recs[i].name = name;
+    tl_prof_first = c->prof_recs.size();
+}
+
+static int prof_event(Context *c) {
     if (c->prof_used == (int)c->prof_pool.size()) {
         hipEvent_t e;
         if (hipEventCreate(&e) != hipSuccess) return -1;
         c->prof_pool.push_back(e);
     }
-    const int i = c->prof_used++;
-    // Inside stream capture the event becomes an external record node of the graph, so
-    // every replay re-records it and reading after a replay times that replay's stages.
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    (void)hipStreamIsCapturing(s, &cap);
-    hipError_t e = cap == hipStreamCaptureStatusActive
-                       ? hipEventRecordWithFlags(c->prof_pool[i], s, hipEventRecordExternal)
-                       : hipEventRecord(c->prof_pool[i], s);
-    if (e != hipSuccess) return -1;
-    return i;
+    return c->prof_used++;
 }
 
-void prof_begin(Context *c, hipStream_t s) {
-    if (!c->profiling) return;
-    c->prof_last = prof_event(c, s);
-}
-
-void prof_mark(Context *c, hipStream_t s, const char *name) {
-    if (!c->profiling || c->prof_last < 0) return;
-    const int e = prof_event(c, s);
-    if (e < 0) return;
-    c->prof_recs.push_back({c->prof_last, e, name});
-    c->prof_last = e;
+bool prof_events(hipEvent_t *start, hipEvent_t *stop) {
+    Context *c = tl_prof_ctx;
+    if (!c) return false;
+    // Stream capture cannot hold these event pairs; launch normally while capturing.
+    const int a = prof_event(c), b = prof_event(c);
+    if (a < 0 || b < 0) return false;
+    *start = c->prof_pool[a];
+    *stop = c->prof_pool[b];
+    c->prof_recs.push_back({a, b, tl_prof_name});
+    return true;
 }
 
 static Context *as_ctx(void *p) {
@@ -501,7 +510,7 @@ __attribute__((visibility("default"))) int dih_qmv(void *ctx, void *matrix, cons
     sg.ids = experts; sg.count = count; sg.x = x; sg.x_bf16 = x_dtype == DIH_BF16;
     sg.x_slot_stride = batched ? m->columns : 0; sg.y = y; sg.y_bf16 = y_dtype == DIH_BF16;
     hipStream_t s = pick(c, stream);
-    prof_begin(c, s);
+    ProfScope prof_scope(c);
     bool ok = launch_qmv(&sg, 1, m->bits, nullptr, s, error, capacity);
     prof_mark(c, s, "qmv");
     return ok ? 0 : -1;
@@ -523,7 +532,7 @@ __attribute__((visibility("default"))) int dih_qmv_swiglu(void *ctx, void *gate_
     sg.p1 = up->packed(); sg.s1 = up->scales(); sg.b1 = up->biases();
     sg.ids = experts; sg.count = count; sg.x = x; sg.x_bf16 = x_dtype == DIH_BF16; sg.y = act;
     hipStream_t s = pick(c, stream);
-    prof_begin(c, s);
+    ProfScope prof_scope(c);
     bool ok = launch_qmv(&sg, 1, gate->bits, nullptr, s, error, capacity);
     prof_mark(c, s, "qmv_swiglu");
     return ok ? 0 : -1;
@@ -575,7 +584,7 @@ __attribute__((visibility("default"))) int dih_lm_head(void *ctx, void *const *s
     uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
     if (!pv || !pi || !tk) return -1;
     hipStream_t s = pick(c, stream);
-    prof_begin(c, s);
+    ProfScope prof_scope(c);
     long offset = 0;
     for (int i = 0; i < slice_count; i += 4) {
         QmvSeg segs[4];
@@ -710,15 +719,15 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
     uint32_t *status = static_cast<uint32_t *>(scratch(c, S_STATUS, 16, error, capacity));
     if (!lg || !srt || !sact || !act || !sout || !ids || !probs || !tk || !status) return -1;
     hipStream_t s = pick(c, stream);
-    prof_begin(c, s);
+    ProfScope prof_scope(c);
     const float *use_logits = logits ? logits : lg;
     // Stage 1: router logits, shared-expert gate GEMV and shared gate/up SwiGLU share x;
     // the last block of the launch that holds the router selects the experts.
     QmvSeg s1[3];
     int n8 = 0;
-    Top8Epilogue tp;
+    Top8Source tp;
     tp.logits = use_logits; tp.experts = E; tp.ids = ids; tp.probs = probs; tp.status = trace ? trace->status : nullptr;
-    tp.ticket = tk;
+    (void)tk;
     if (router) {
         QmvSeg a = seg_of(router);
         a.x = x; a.x_bf16 = 1; a.y = lg;
@@ -733,20 +742,21 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
     int nrest = 0;
     if (sr->bits == 8) s1[n8++] = b; else rest[nrest++] = b;
     if (sg->bits == 8) s1[n8++] = g; else rest[nrest++] = g;
-    if (n8 && !launch_qmv(s1, n8, 8, &tp, s, error, capacity)) return -1;
-    if (nrest && !launch_qmv(rest, nrest, 5, n8 ? nullptr : &tp, s, error, capacity)) return -1;
+    if (n8 && !launch_qmv(s1, n8, 8, nullptr, s, error, capacity)) return -1;
+    if (nrest && !launch_qmv(rest, nrest, 5, nullptr, s, error, capacity)) return -1;
     prof_mark(c, s, "decode_router_shared");
-    // Stage 2: selected experts' gate/up SwiGLU and the shared down projection.
+    // Stage 2: every wave selects the top-8 from the logits, then the selected experts'
+    // gate/up SwiGLU; the shared down projection shares the launch.
     QmvSeg e2 = seg_of(gate);
     e2.p1 = up->packed(); e2.s1 = up->scales(); e2.b1 = up->biases();
-    e2.ids = ids; e2.count = 8; e2.x = x; e2.x_bf16 = 1; e2.y = act;
+    e2.top8 = 1; e2.count = 8; e2.x = x; e2.x_bf16 = 1; e2.y = act;
     QmvSeg d2 = seg_of(sd);
     d2.x = sact; d2.y = sout;
     if (sd->bits == gate->bits && cpl_of(sd->columns) == cpl_of(gate->columns)) {
         QmvSeg both[2] = {e2, d2};
-        if (!launch_qmv(both, 2, gate->bits, nullptr, s, error, capacity)) return -1;
+        if (!launch_qmv(both, 2, gate->bits, &tp, s, error, capacity)) return -1;
     } else {
-        if (!launch_qmv(&e2, 1, gate->bits, nullptr, s, error, capacity) ||
+        if (!launch_qmv(&e2, 1, gate->bits, &tp, s, error, capacity) ||
             !launch_qmv(&d2, 1, sd->bits, nullptr, s, error, capacity))
             return -1;
     }
@@ -803,7 +813,7 @@ __attribute__((visibility("default"))) int dih_moe_prefill(void *ctx, const dih_
     if (!ids || !probs || !counts || !routes || !chunks || !nch || !tk || !actb || !rout) return -1;
     float *route_out = trace && trace->expert_out ? trace->expert_out : rout;
     hipStream_t s = pick(c, stream);
-    prof_begin(c, s);
+    ProfScope prof_scope(c);
     if (!launch_top8(logits, logits_dtype == DIH_BF16, tokens, E, ids, probs, trace ? trace->status : nullptr,
                      trace ? trace->logits : nullptr, tk + 3, s, error, capacity))
         return -1;
@@ -850,7 +860,7 @@ __attribute__((visibility("default"))) int dih_dense(void *ctx, void *matrix, in
     a.m0 = m; a.tokens = tokens; a.dense = 1; a.x = static_cast<const uint16_t *>(x); a.in_mode = 0;
     a.y = y; a.y_bf16 = y_dtype == DIH_BF16;
     hipStream_t s = pick(c, stream);
-    prof_begin(c, s);
+    ProfScope prof_scope(c);
     bool ok = launch_qmm(a, s, error, capacity);
     prof_mark(c, s, "dense_qmm");
     return ok ? 0 : -1;
@@ -863,7 +873,6 @@ __attribute__((visibility("default"))) int dih_set_profiling(void *ctx, int enab
     c->profiling = enabled != 0;
     c->prof_recs.clear();
     c->prof_used = 0;
-    c->prof_last = -1;
     return 0;
 }
 

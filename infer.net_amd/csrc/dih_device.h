@@ -13,6 +13,7 @@
 
 #define DIH_DEV __device__ __forceinline__
 
+
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short dih_bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float dih_f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float dih_f32x4;
@@ -92,28 +93,103 @@ DIH_DEV void chunk_to_bf16(const Chunk<BITS> &c, float scale, float bias, dih_bf
     }
 }
 
-// Sum over aligned groups of `width` lanes (width a power of two, <= 64).
-DIH_DEV float group_sum(float v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// ---- cross-lane all-reduce without LDS (gfx950) ----
+// Within 16-lane rows: DPP quad_perm [1,0,3,2] and [2,3,0,1] (xor 1, xor 2),
+// row_half_mirror (lane i <-> 7-i in each 8-lane half: joins quads 0 and 1) and row_mirror
+// (lane i <-> 15-i: joins the two 8-lane halves). Across rows: v_permlane16_swap pairs rows
+// (0,1),(2,3) and v_permlane32_swap pairs the wave halves; with both operands equal, the sum
+// (or max/min) of the two returned registers is the pair's combination in every lane.
+#define DIH_DPP_XOR1 0xB1
+#define DIH_DPP_XOR2 0x4E
+#define DIH_DPP_HALF_MIRROR 0x141
+#define DIH_DPP_MIRROR 0x140
+
+template <int CTRL>
+DIH_DEV uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
-DIH_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+template <int CTRL>
+DIH_DEV float dppf(float v) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, v)));
 }
-DIH_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-DIH_DEV uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t w = (uint32_t)__shfl_xor((int)v, o, 64);
-        v = w < v ? w : v;
+
+struct OpAdd { DIH_DEV float operator()(float a, float b) const { return a + b; } };
+struct OpMax { DIH_DEV float operator()(float a, float b) const { return fmaxf(a, b); } };
+
+// All-reduce of a float over aligned groups of `width` lanes (power of two <= 64); every
+// lane of a group receives the group's result.
+template <typename Op>
+DIH_DEV float group_reduce(float v, int width, Op op) {
+    if (width >= 2) v = op(v, dppf<DIH_DPP_XOR1>(v));
+    if (width >= 4) v = op(v, dppf<DIH_DPP_XOR2>(v));
+    if (width >= 8) v = op(v, dppf<DIH_DPP_HALF_MIRROR>(v));
+    if (width >= 16) v = op(v, dppf<DIH_DPP_MIRROR>(v));
+    if (width >= 32) {
+        uint32_t u = __builtin_bit_cast(uint32_t, v);
+        auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        v = op(__builtin_bit_cast(float, (uint32_t)p[0]), __builtin_bit_cast(float, (uint32_t)p[1]));
+    }
+    if (width >= 64) {
+        uint32_t u = __builtin_bit_cast(uint32_t, v);
+        auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        v = op(__builtin_bit_cast(float, (uint32_t)p[0]), __builtin_bit_cast(float, (uint32_t)p[1]));
     }
     return v;
+}
+DIH_DEV float group_sum(float v, int width) { return group_reduce(v, width, OpAdd()); }
+DIH_DEV float wave_sum(float v) { return group_reduce(v, 64, OpAdd()); }
+DIH_DEV float wave_max(float v) { return group_reduce(v, 64, OpMax()); }
+
+DIH_DEV uint32_t umin_(uint32_t a, uint32_t b) { return a < b ? a : b; }
+DIH_DEV uint32_t wave_min_u32(uint32_t v) {
+    v = umin_(v, dpp<DIH_DPP_XOR1>(v));
+    v = umin_(v, dpp<DIH_DPP_XOR2>(v));
+    v = umin_(v, dpp<DIH_DPP_HALF_MIRROR>(v));
+    v = umin_(v, dpp<DIH_DPP_MIRROR>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = umin_((uint32_t)p[0], (uint32_t)p[1]);
+    auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return umin_((uint32_t)q[0], (uint32_t)q[1]);
+}
+
+// Top-8 of up to 256 logits by one wave (graph_top8 gpu_graph.mm:134-146 semantics:
+// repeated wave max, ties to the lowest id; softmax over the chosen eight with the first
+// (largest) subtracted, summed in slot order). Every lane receives ids/probs. `bad` is
+// set when a logit is not finite (the ids are then 0..7 order-free zeros: all 0).
+DIH_DEV void wave_top8(const float *logits, int experts, uint32_t (&ids)[8], float (&probs)[8],
+                       bool &bad) {
+    const int lane = threadIdx.x & 63;
+    float cand[4];
+    bool nf = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        float v = e < experts ? logits[e] : -INFINITY;
+        if (e < experts && !isfinite(v)) nf = true;
+        cand[j] = v;
+    }
+    bad = __any(nf);
+    float chosen[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        float best = cand[0];
+        uint32_t id = (uint32_t)lane;
+#pragma unroll
+        for (int j = 1; j < 4; j++)
+            if (cand[j] > best) { best = cand[j]; id = (uint32_t)(lane + 64 * j); }
+        const float m = wave_max(best);
+        const uint32_t sel = wave_min_u32(best == m ? id : 0xffffffffu);
+        chosen[n] = m;
+        ids[n] = bad ? 0u : sel;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if ((uint32_t)(lane + 64 * j) == sel) cand[j] = -INFINITY;
+    }
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { probs[i] = __expf(chosen[i] - chosen[0]); total += probs[i]; }
+#pragma unroll
+    for (int i = 0; i < 8; i++) probs[i] = probs[i] / total;
 }
 
 DIH_DEV float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }

@@ -1,6 +1,7 @@
 // Host-side internals of libdeepinfer_hip: context and matrix objects, scratch
 // management, kernel launchers shared between translation units.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -44,14 +45,13 @@ struct Context {
     hipEvent_t start = nullptr, stop = nullptr;
     bool resident = false;
     uint64_t weight_bytes = 0;
-    // profiling: events recorded on the call's stream between the stages of every
-    // device-resident call; aggregated per stage name when read
+    // profiling: one start/stop event pair per kernel launch of device-resident calls,
+    // aggregated per stage name when read
     bool profiling = false;
     std::vector<hipEvent_t> prof_pool;        // reused across resets
     struct ProfRec { int begin, end; const char *name; };
     std::vector<ProfRec> prof_recs;
     int prof_used = 0;                        // events taken from the pool since reset
-    int prof_last = -1;                       // event that closes the previous stage
     // named scratch
     Scratch ws[24];
     uint32_t magic = 0x44494358u;
@@ -69,9 +69,32 @@ bool hip_ok(hipError_t e, char *error, int capacity, const char *what);
 void *scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity);
 bool sync_matrix(Matrix *m, char *error, int capacity);
 
-// Profiling helpers: stage boundaries on `stream`.
-void prof_begin(Context *c, hipStream_t s);
-void prof_mark(Context *c, hipStream_t s, const char *name);
+// Profiling. While a ProfScope for a profiling context is alive on this thread, every
+// launch goes through hipExtLaunchKernelGGL with a start/stop event pair taken from the
+// context's pool; the command processor stamps those events at the kernel's own start
+// and end, so the recorded interval is the kernel alone (no host or queue gaps). The
+// record carries the stage name set by prof_stage().
+struct ProfScope {
+    explicit ProfScope(Context *c);
+    ~ProfScope();
+};
+void prof_stage(const char *name);
+bool prof_events(hipEvent_t *start, hipEvent_t *stop);  // false when not profiling
+
+// Launch with the thread's sticky HIP error cleared first, so that the hipGetLastError()
+// check after the launch reports this launch only (another runtime user, e.g. the
+// caller's own HIP calls, can leave an unread error behind).
+template <typename... KArgs, typename... Args>
+void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t s,
+            Args... args) {
+    (void)hipGetLastError();
+    hipEvent_t a, b;
+    if (prof_events(&a, &b))
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, a, b, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+}
+#define DIH_LAUNCH(kernel, ...) ::dih::launch(kernel, __VA_ARGS__)
 
 // ---- launchers (defined in the .hip translation units) ----
 
@@ -83,17 +106,18 @@ struct QmvSeg {
     const uint32_t *ids = nullptr;  // device expert ids or null (expert 0)
     int rows = 0, columns = 0, count = 1;
     int experts = 1;                // ids >= experts produce NaN outputs (no fault)
+    int top8 = 0;                   // 1: slot ids are the top-8 of Top8Source::logits
     const void *x = nullptr; int x_bf16 = 0; int x_slot_stride = 0;  // elements
     void *y = nullptr; int y_bf16 = 0;
 };
-// Launches up to 4 segments of equal bit width in one kernel. `top8` (optional) makes
-// the last finishing block select experts from `top8_logits`.
-struct Top8Epilogue {
+// Launches up to 4 segments of equal bit width in one kernel. A segment flagged `top8`
+// takes its 8 slot experts from the top-8 of `logits` (every wave selects them itself; the
+// segment's first wave publishes ids/probs/status for later kernels).
+struct Top8Source {
     const float *logits = nullptr; int experts = 0;
     uint32_t *ids = nullptr; float *probs = nullptr; uint32_t *status = nullptr;
-    uint32_t *ticket = nullptr;
 };
-bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Epilogue *top8,
+bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8,
                 hipStream_t s, char *error, int capacity);
 
 bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t *ids,

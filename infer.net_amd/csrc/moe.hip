@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void top8_kernel(const void *logits, int logit
 bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, uint32_t *ids,
                  float *probs, uint32_t *status, float *logits_copy, uint32_t *zero_word,
                  hipStream_t s, char *error, int capacity) {
-    hipLaunchKernelGGL(top8_kernel, dim3((tokens + 3) / 4), dim3(256), 0, s, logits, logits_bf16,
+    DIH_LAUNCH(top8_kernel, dim3((tokens + 3) / 4), dim3(256), 0, s, logits, logits_bf16,
                        tokens, experts, ids, probs, status, logits_copy, zero_word);
     return hip_ok(hipGetLastError(), error, capacity, "top8 launch");
 }
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void group_kernel(const uint32_t *ids, int tok
 bool launch_build_groups(const uint32_t *ids, int tokens, int experts, int with_shared,
                          uint32_t *counts, uint32_t *routes, int4 *chunks, uint32_t *nchunks,
                          uint32_t *ticket, hipStream_t s, char *error, int capacity) {
-    hipLaunchKernelGGL(group_kernel, dim3(experts + with_shared), dim3(256), 0, s, ids, tokens,
+    DIH_LAUNCH(group_kernel, dim3(experts + with_shared), dim3(256), 0, s, ids, tokens,
                        experts, with_shared, counts, routes, chunks, nchunks, ticket);
     return hip_ok(hipGetLastError(), error, capacity, "grouping launch");
 }
@@ -199,11 +199,11 @@ bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens,
                       const float *route_out, const float *probs, uint16_t *residual,
                       hipStream_t s, char *error, int capacity) {
     if (shared_route->bits == 8)
-        hipLaunchKernelGGL((merge_kernel<8>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
+        DIH_LAUNCH((merge_kernel<8>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
                            shared_route->scales(), shared_route->biases(), x, tokens, hidden, route_out,
                            probs, residual);
     else
-        hipLaunchKernelGGL((merge_kernel<5>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
+        DIH_LAUNCH((merge_kernel<5>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
                            shared_route->scales(), shared_route->biases(), x, tokens, hidden, route_out,
                            probs, residual);
     return hip_ok(hipGetLastError(), error, capacity, "merge launch");
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *v, int n, floa
 bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
                    uint32_t *ticket, uint32_t *next, hipStream_t s, char *error, int capacity) {
     const int blocks = (n + 1023) / 1024;
-    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, values, n, part_val, part_idx,
+    DIH_LAUNCH(argmax_kernel, dim3(blocks), dim3(256), 0, s, values, n, part_val, part_idx,
                        ticket, next);
     return hip_ok(hipGetLastError(), error, capacity, "argmax launch");
 }

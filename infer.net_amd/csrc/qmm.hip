@@ -216,11 +216,11 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     dim3 grid((unsigned)blocks), block(256);
     const bool gated = m1 != nullptr;
     if (m0->bits == 8) {
-        if (gated) hipLaunchKernelGGL((qmm_kernel<8, true, 2>), grid, block, 0, s, P);
-        else hipLaunchKernelGGL((qmm_kernel<8, false, 2>), grid, block, 0, s, P);
+        if (gated) DIH_LAUNCH((qmm_kernel<8, true, 2>), grid, block, 0, s, P);
+        else DIH_LAUNCH((qmm_kernel<8, false, 2>), grid, block, 0, s, P);
     } else {
-        if (gated) hipLaunchKernelGGL((qmm_kernel<5, true, 2>), grid, block, 0, s, P);
-        else hipLaunchKernelGGL((qmm_kernel<5, false, 2>), grid, block, 0, s, P);
+        if (gated) DIH_LAUNCH((qmm_kernel<5, true, 2>), grid, block, 0, s, P);
+        else DIH_LAUNCH((qmm_kernel<5, false, 2>), grid, block, 0, s, P);
     }
     return hip_ok(hipGetLastError(), error, capacity, "qmm launch");
 }

@@ -2,19 +2,25 @@
 //
 // Mapping: a row of C columns is split into C/32 lane chunks (32 codes = half of one
 // affine group). `lpr` lanes (a power of two <= 64) share a row; a wave therefore works
-// on 64/lpr rows at once and each lane owns CPL chunks of its row. Row sums use the
-// identity  sum_c (q_c*s_g + b_g)*x_c = s_g*sum_c q_c*x_c + b_g*sum_c x_c  per chunk, so
-// the inner loop is one code extraction/convert and one FMA per code; sum_c x_c is
-// computed once per lane per launch. This is the semantics of quant_rows / quant_dot
-// (quantized.mm:83-144) and expert_gate_up (quantized.mm:148-189), re-tiled for wave64
-// and 16-byte loads rather than translated.
+// on 64/lpr rows ("a row group") at once and each lane owns CPL chunks of its row. Row sums
+// use  sum_c (q_c*s_g + b_g)*x_c = s_g*sum_c q_c*x_c + b_g*sum_c x_c  per chunk, so the
+// inner loop is one code extraction/convert and one FMA per code; sum_c x_c is computed
+// once per lane per launch. This is the semantics of quant_rows / quant_dot
+// (quantized.mm:83-144) and expert_gate_up (quantized.mm:148-189), re-tiled for wave64.
+//
+// Latency: each wave walks its row groups (strided by the number of waves of the slot, so
+// the chip reads one contiguous region at a time) with two stages of kU row groups in
+// flight: the weights of stage t+1 are requested before stage t is reduced. The grid is
+// sized to about four blocks per CU so every wave is resident from the start. Weight loads
+// are issued before the activation loads and nothing waits on a cross-block fence.
 #include "dih_device.h"
 #include "dih_internal.h"
 
 namespace dih {
 
 constexpr int kMaxSeg = 4;
-constexpr int kRowsPerLaneGroup = 2;  // rows in flight per lane group
+constexpr int kU = 2;              // row groups per pipeline stage
+constexpr int kBlocksTarget = 1024;  // ~4 blocks of 256 threads per CU on 256 CUs
 
 struct QmvParams {
     QmvSeg seg[kMaxSeg];
@@ -22,52 +28,14 @@ struct QmvParams {
     int lpr[kMaxSeg];
     int blocks_per_slot[kMaxSeg];
     int nseg;
-    Top8Epilogue top8;
+    Top8Source top8;
 };
 
-// Top-8 of up to 256 logits by one wave (graph_top8 gpu_graph.mm:134-146 semantics:
-// repeated wave max, ties to the lowest id; softmax over the chosen eight with the
-// first (largest) subtracted, summed in slot order).
-DIH_DEV void wave_top8(const float *logits, int experts, uint32_t *ids, float *probs,
-                       uint32_t *status, int lane) {
-    float cand[4];
-    bool bad = false;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int e = lane + 64 * j;
-        float v = e < experts ? logits[e] : -INFINITY;
-        if (e < experts && !isfinite(v)) bad = true;
-        cand[j] = v;
-    }
-    bool any_bad = __any(bad);
-    float chosen[8];
-    uint32_t picked[8];
-#pragma unroll
-    for (int n = 0; n < 8; n++) {
-        float best = cand[0];
-        uint32_t id = (uint32_t)lane;
-#pragma unroll
-        for (int j = 1; j < 4; j++)
-            if (cand[j] > best) { best = cand[j]; id = (uint32_t)(lane + 64 * j); }
-        float m = wave_max(best);
-        uint32_t sel = wave_min_u32(best == m ? id : 0xffffffffu);
-        chosen[n] = m;
-        picked[n] = sel;
-        if ((int)(sel & 63u) == lane) {
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if ((uint32_t)(lane + 64 * j) == sel) cand[j] = -INFINITY;
-        }
-    }
-    if (lane == 0) {
-        float p[8], total = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) { p[i] = __expf(chosen[i] - chosen[0]); total += p[i]; }
-#pragma unroll
-        for (int i = 0; i < 8; i++) { ids[i] = any_bad ? 0u : picked[i]; probs[i] = p[i] / total; }
-        if (status && any_bad) *status = 1u;
-    }
-}
+template <int BITS, int CPL>
+struct Stage {
+    Chunk<BITS> w[kU][CPL], u[kU][CPL];
+    float s[kU][CPL], b[kU][CPL], su[kU][CPL], bu[kU][CPL];
+};
 
 template <int BITS, int CPL>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
@@ -82,14 +50,68 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     const int slot = local / P.blocks_per_slot[k];
     const int rb = local - slot * P.blocks_per_slot[k];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rpw = 64 / lpr;  // row groups per wave
+    const int rpw = 64 / lpr;  // rows per row group
     const int g = lane / lpr, j = lane - g * lpr;
     const int nchunk = S.columns >> 5;
-    const int rows_per_block = 4 * rpw * kRowsPerLaneGroup;
-    uint32_t e = S.ids ? S.ids[slot] : 0u;
+    const bool gated = S.p1 != nullptr;
+
+    // Expert of this slot: a device id, or top-8 of the router logits computed by this
+    // wave (the first wave of the segment publishes ids/probs for the next kernel).
+    uint32_t e = 0u;
+    if (S.top8) {
+        uint32_t ids[8];
+        float probs[8];
+        bool bad;
+        wave_top8(P.top8.logits, P.top8.experts, ids, probs, bad);
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (q == slot) e = ids[q];
+        if (local == 0 && wave == 0 && lane < 8) {
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (q == lane) { P.top8.ids[q] = ids[q]; P.top8.probs[q] = probs[q]; }
+            if (lane == 0 && bad && P.top8.status) *P.top8.status = 1u;
+        }
+    } else if (S.ids) {
+        e = S.ids[slot];
+    }
     const bool bad_id = e >= (uint32_t)S.experts;
     if (bad_id) e = 0u;
     const size_t wpr = (size_t)S.columns * BITS / 32, gpr = (size_t)(S.columns >> 6);
+    const size_t ebase = (size_t)e * S.rows;
+
+    const int groups_total = (S.rows + rpw - 1) / rpw;
+    const int W = P.blocks_per_slot[k] * 4;
+    const int wi = rb * 4 + wave;
+    const int stride = W * kU;
+    const int iters = wi < groups_total ? (groups_total - wi + stride - 1) / stride : 0;
+
+    auto load = [&](Stage<BITS, CPL> &st, int it) {
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            int r = (wi + (it * kU + u) * W) * rpw + g;
+            r = r < S.rows ? r : S.rows - 1;
+            const size_t rowi = ebase + r;
+            const uint32_t *wrow = S.p0 + rowi * wpr;
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+                const int ch = j + c * lpr;
+                if (ch < nchunk) {
+                    load_chunk<BITS>(st.w[u][c], wrow, ch);
+                    st.s[u][c] = bf16_to_f32(S.s0[rowi * gpr + (ch >> 1)]);
+                    st.b[u][c] = bf16_to_f32(S.b0[rowi * gpr + (ch >> 1)]);
+                    if (gated) {
+                        load_chunk<BITS>(st.u[u][c], S.p1 + rowi * wpr, ch);
+                        st.su[u][c] = bf16_to_f32(S.s1[rowi * gpr + (ch >> 1)]);
+                        st.bu[u][c] = bf16_to_f32(S.b1[rowi * gpr + (ch >> 1)]);
+                    }
+                }
+            }
+        }
+    };
+
+    Stage<BITS, CPL> A, B;
+    if (iters > 0) load(A, 0);
 
     // This lane's activations and their chunk sums.
     float xr[CPL][32];
@@ -111,72 +133,38 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
         }
     }
 
-    const bool gated = S.p1 != nullptr;
-    int rows[kRowsPerLaneGroup];
-    Chunk<BITS> wc[kRowsPerLaneGroup][CPL], uc[kRowsPerLaneGroup][CPL];
-    float sc[kRowsPerLaneGroup][CPL], bc[kRowsPerLaneGroup][CPL];
-    float su[kRowsPerLaneGroup][CPL], bu[kRowsPerLaneGroup][CPL];
+    auto consume = [&](const Stage<BITS, CPL> &st, int it) {
 #pragma unroll
-    for (int u = 0; u < kRowsPerLaneGroup; u++) {
-        int r = rb * rows_per_block + (wave * kRowsPerLaneGroup + u) * rpw + g;
-        rows[u] = r;
-        int rr = r < S.rows ? r : S.rows - 1;
-        const size_t rowi = (size_t)e * S.rows + rr;
-        const uint32_t *wrow = S.p0 + rowi * wpr;
+        for (int u = 0; u < kU; u++) {
+            const int r = (wi + (it * kU + u) * W) * rpw + g;
+            float a = 0.f, b = 0.f;
 #pragma unroll
-        for (int c = 0; c < CPL; c++) {
-            const int ch = j + c * lpr;
-            if (ch < nchunk) {
-                load_chunk<BITS>(wc[u][c], wrow, ch);
-                sc[u][c] = bf16_to_f32(S.s0[rowi * gpr + (ch >> 1)]);
-                bc[u][c] = bf16_to_f32(S.b0[rowi * gpr + (ch >> 1)]);
-                if (gated) {
-                    load_chunk<BITS>(uc[u][c], S.p1 + rowi * wpr, ch);
-                    su[u][c] = bf16_to_f32(S.s1[rowi * gpr + (ch >> 1)]);
-                    bu[u][c] = bf16_to_f32(S.b1[rowi * gpr + (ch >> 1)]);
+            for (int c = 0; c < CPL; c++) {
+                const int ch = j + c * lpr;
+                if (ch < nchunk) {
+                    a += st.s[u][c] * chunk_dot<BITS>(st.w[u][c], xr[c]) + st.b[u][c] * xs[c];
+                    if (gated) b += st.su[u][c] * chunk_dot<BITS>(st.u[u][c], xr[c]) + st.bu[u][c] * xs[c];
                 }
             }
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < kRowsPerLaneGroup; u++) {
-        float a = 0.f, b = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPL; c++) {
-            const int ch = j + c * lpr;
-            if (ch < nchunk) {
-                a += sc[u][c] * chunk_dot<BITS>(wc[u][c], xr[c]) + bc[u][c] * xs[c];
-                if (gated) b += su[u][c] * chunk_dot<BITS>(uc[u][c], xr[c]) + bu[u][c] * xs[c];
+            a = group_sum(a, lpr);
+            if (gated) b = group_sum(b, lpr);
+            if (j == 0 && r < S.rows) {
+                const float v = bad_id ? __builtin_nanf("") : (gated ? siluf_(a) * b : a);
+                const size_t o = (size_t)slot * S.rows + r;
+                if (S.y_bf16)
+                    static_cast<uint16_t *>(S.y)[o] = f32_to_bf16(v);
+                else
+                    static_cast<float *>(S.y)[o] = v;
             }
         }
-        a = group_sum(a, lpr);
-        if (gated) b = group_sum(b, lpr);
-        if (j == 0 && rows[u] < S.rows) {
-            float v = bad_id ? __builtin_nanf("") : (gated ? siluf_(a) * b : a);
-            size_t o = (size_t)slot * S.rows + rows[u];
-            if (S.y_bf16)
-                static_cast<uint16_t *>(S.y)[o] = f32_to_bf16(v);
-            else
-                static_cast<float *>(S.y)[o] = v;
-        }
-    }
+    };
 
-    if (P.top8.ticket) {
-        __shared__ int last;
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned t = atomicAdd(P.top8.ticket, 1u);
-            last = (t == gridDim.x - 1);
-        }
-        __syncthreads();
-        if (last) {
-            __threadfence();
-            if (wave == 0) {
-                wave_top8(P.top8.logits, P.top8.experts, P.top8.ids, P.top8.probs,
-                          P.top8.status, lane);
-                if (lane == 0) *P.top8.ticket = 0u;
-            }
+    for (int it = 0; it < iters; it += 2) {
+        if (it + 1 < iters) load(B, it + 1);
+        consume(A, it);
+        if (it + 1 < iters) {
+            if (it + 2 < iters) load(A, it + 2);
+            consume(B, it + 1);
         }
     }
 }
@@ -187,34 +175,49 @@ static int pow2ceil(int v) {
     return p;
 }
 
-bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Epilogue *top8,
-                hipStream_t s, char *error, int capacity) {
+bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, hipStream_t s,
+                char *error, int capacity) {
     if (nseg < 1 || nseg > kMaxSeg) {
         set_error(error, capacity, "Invalid GEMV segment count");
         return false;
     }
     QmvParams P{};
     P.nseg = nseg;
-    int cpl = 1, blocks = 0;
+    int cpl = 1;
+    long want = 0;
+    long groups[kMaxSeg];
     for (int i = 0; i < nseg; i++) {
         P.seg[i] = segs[i];
-        int nchunk = segs[i].columns / 32;
-        int lpr = nchunk >= 64 ? 64 : pow2ceil(nchunk);
-        int c = (nchunk + 63) / 64;
+        if (segs[i].top8 && (!top8 || !top8->logits || segs[i].count != 8)) {
+            set_error(error, capacity, "Router selection segment without logits");
+            return false;
+        }
+        const int nchunk = segs[i].columns / 32;
+        const int lpr = nchunk >= 64 ? 64 : pow2ceil(nchunk);
+        const int c = (nchunk + 63) / 64;
         if (c > cpl) cpl = c;
         P.lpr[i] = lpr;
-        int rows_per_block = 4 * (64 / lpr) * kRowsPerLaneGroup;
-        P.blocks_per_slot[i] = (segs[i].rows + rows_per_block - 1) / rows_per_block;
+        groups[i] = (segs[i].rows + (64 / lpr) - 1) / (64 / lpr);
+        want += ((groups[i] + 4 * kU - 1) / (4 * kU)) * segs[i].count;
+    }
+    // Blocks per slot: enough for one stage per wave, capped near kBlocksTarget overall
+    // (each wave then walks several stages with the next one in flight).
+    int blocks = 0;
+    for (int i = 0; i < nseg; i++) {
+        long full = (groups[i] + 4 * kU - 1) / (4 * kU);
+        long bps = full;
+        if (want > kBlocksTarget) bps = std::max(1L, (full * kBlocksTarget + want - 1) / want);
+        P.blocks_per_slot[i] = (int)bps;
         P.start[i] = blocks;
-        blocks += P.blocks_per_slot[i] * segs[i].count;
+        blocks += (int)bps * segs[i].count;
     }
     P.start[nseg] = blocks;
     if (top8) P.top8 = *top8;
     dim3 grid(blocks), block(256);
-#define DIH_QMV_CASE(B, C)                                                   \
-    if (bits == B && cpl <= C) {                                             \
-        hipLaunchKernelGGL((qmv_kernel<B, C>), grid, block, 0, s, P);        \
-        return hip_ok(hipGetLastError(), error, capacity, "qmv launch");     \
+#define DIH_QMV_CASE(B, C)                                                \
+    if (bits == B && cpl <= C) {                                          \
+        DIH_LAUNCH((qmv_kernel<B, C>), grid, block, 0, s, P);             \
+        return hip_ok(hipGetLastError(), error, capacity, "qmv launch");  \
     }
     DIH_QMV_CASE(8, 1)
     DIH_QMV_CASE(8, 2)
@@ -231,57 +234,66 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Epilogue *top8
 // (quant_rows batched down + graph_merge_norm's weighted sum, gpu_graph.mm:48-61, and
 // Qwen36Model.cs:242-244): y = sigmoid(sroute)*shared_out[h] + sum_{slot 0..7}
 // p_slot * (down[e_slot][h] . act[slot]); residual[h] = bf16(residual[h] + y).
-// lpr lanes per slot-row; a wave covers 64/lpr slots per pass.
-template <int BITS>
-__global__ __launch_bounds__(256) void moe_down_merge_kernel(
+// A block of eight waves owns ROWS output rows; wave w computes slot w for all of them
+// (its activation chunk is loaded once), the slot results meet in LDS and the first ROWS
+// threads merge them in slot order.
+template <int BITS, int LPR>
+__global__ __launch_bounds__(512) void moe_down_merge_kernel(
     const uint32_t *__restrict__ packed, const uint16_t *__restrict__ scales,
     const uint16_t *__restrict__ biases, int H, int I, const float *__restrict__ act,
     const uint32_t *__restrict__ ids, const float *__restrict__ probs,
     const float *__restrict__ shared_out, const float *__restrict__ sroute,
-    uint16_t *__restrict__ residual, float *__restrict__ route_out, int lpr, int rows_per_wave) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int groups = 64 / lpr, g = lane / lpr, j = lane - g * lpr;
+    uint16_t *__restrict__ residual, float *__restrict__ route_out) {
+    constexpr int GROUPS = 64 / LPR;                      // rows per pass of a wave
+    constexpr int ROWS = GROUPS > 16 ? GROUPS : 16;       // output rows per block
+    constexpr int PASSES = ROWS / GROUPS;
+    __shared__ float part[8][ROWS];
+    const int slot = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane / LPR, j = lane - g * LPR;
     const int nchunk = I >> 5;
-    const int passes = (8 + groups - 1) / groups;
     const size_t wpr = (size_t)I * BITS / 32, gpr = (size_t)(I >> 6);
-    const int row0 = (blockIdx.x * 4 + wave) * rows_per_wave;
-    for (int rr = 0; rr < rows_per_wave; rr++) {
-        const int h = row0 + rr;
-        if (h >= H) break;
-        float mine[8];
+    const int row0 = blockIdx.x * ROWS;
+    const uint32_t e = ids[slot];
+    // weights first: every pass of this wave in flight at once
+    Chunk<BITS> wc[PASSES];
+    float sc[PASSES], bc[PASSES];
 #pragma unroll
-        for (int p = 0; p < 8; p++) mine[p] = 0.f;
-        for (int p = 0; p < passes; p++) {
-            const int slot = p * groups + g;
-            float v = 0.f;
-            if (slot < 8 && j < nchunk) {
-                const uint32_t e = ids[slot];
-                const size_t rowi = (size_t)e * H + h;
-                Chunk<BITS> wc;
-                load_chunk<BITS>(wc, packed + rowi * wpr, j);
-                float xr[32];
-                load_x32(xr, act + (size_t)slot * I, 0, j * 32);
-                float xs = 0.f;
-#pragma unroll
-                for (int i = 0; i < 32; i++) xs += xr[i];
-                v = bf16_to_f32(scales[rowi * gpr + (j >> 1)]) * chunk_dot<BITS>(wc, xr) +
-                    bf16_to_f32(biases[rowi * gpr + (j >> 1)]) * xs;
-            }
-            v = group_sum(v, lpr);
-            // gather slot results of this pass into every lane
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                if (q / groups == p) mine[q] = __shfl(v, (q % groups) * lpr, 64);
+    for (int p = 0; p < PASSES; p++) {
+        int h = row0 + p * GROUPS + g;
+        h = h < H ? h : H - 1;
+        const size_t rowi = (size_t)e * H + h;
+        if (j < nchunk) {
+            load_chunk<BITS>(wc[p], packed + rowi * wpr, j);
+            sc[p] = bf16_to_f32(scales[rowi * gpr + (j >> 1)]);
+            bc[p] = bf16_to_f32(biases[rowi * gpr + (j >> 1)]);
         }
-        if (lane == 0) {
-            float y = shared_out[h] * sigmoidf_(sroute[0]);
+    }
+    float xr[32];
+    float xs = 0.f;
+    if (j < nchunk) {
+        load_x32(xr, act + (size_t)slot * I, 0, j * 32);
 #pragma unroll
-            for (int q = 0; q < 8; q++) y += mine[q] * probs[q];
+        for (int i = 0; i < 32; i++) xs += xr[i];
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        float v = j < nchunk ? sc[p] * chunk_dot<BITS>(wc[p], xr) + bc[p] * xs : 0.f;
+        v = group_sum(v, LPR);
+        if (j == 0) part[slot][p * GROUPS + g] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < ROWS) {
+        const int r = threadIdx.x, h = row0 + r;
+        if (h < H) {
+            const float sh = shared_out[h];
+            float y = sh * sigmoidf_(sroute[0]);
+#pragma unroll
+            for (int q = 0; q < 8; q++) y += part[q][r] * probs[q];
             residual[h] = f32_to_bf16(bf16_to_f32(residual[h]) + y);
             if (route_out) {
 #pragma unroll
-                for (int q = 0; q < 8; q++) route_out[(size_t)q * H + h] = mine[q];
-                route_out[(size_t)8 * H + h] = shared_out[h];
+                for (int q = 0; q < 8; q++) route_out[(size_t)q * H + h] = part[q][r];
+                route_out[(size_t)8 * H + h] = sh;
             }
         }
     }
@@ -292,23 +304,26 @@ bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t 
                            uint16_t *residual, float *route_out, hipStream_t s, char *error,
                            int capacity) {
     const int H = down->rows, I = down->columns;
-    int nchunk = I / 32;
+    const int nchunk = I / 32;
     if (nchunk > 64) {
         set_error(error, capacity, "Down projection wider than 2048 columns is not supported");
         return false;
     }
-    int lpr = pow2ceil(nchunk);
-    const int rows_per_wave = 2;
-    int blocks = (H + 4 * rows_per_wave - 1) / (4 * rows_per_wave);
-    if (down->bits == 8)
-        hipLaunchKernelGGL((moe_down_merge_kernel<8>), dim3(blocks), dim3(256), 0, s, down->packed(),
-                           down->scales(), down->biases(), H, I, act, ids, probs, shared_out, sroute,
-                           residual, route_out, lpr, rows_per_wave);
-    else
-        hipLaunchKernelGGL((moe_down_merge_kernel<5>), dim3(blocks), dim3(256), 0, s, down->packed(),
-                           down->scales(), down->biases(), H, I, act, ids, probs, shared_out, sroute,
-                           residual, route_out, lpr, rows_per_wave);
-    return hip_ok(hipGetLastError(), error, capacity, "down/merge launch");
+    const int lpr = pow2ceil(nchunk);
+    const int rows = std::max(16, 64 / lpr);
+    const int blocks = (H + rows - 1) / rows;
+#define DIH_DM_CASE(B, L)                                                                            \
+    if (down->bits == B && lpr == L) {                                                               \
+        DIH_LAUNCH((moe_down_merge_kernel<B, L>), dim3(blocks), dim3(512), 0, s, down->packed(),     \
+                   down->scales(), down->biases(), H, I, act, ids, probs, shared_out, sroute,        \
+                   residual, route_out);                                                             \
+        return hip_ok(hipGetLastError(), error, capacity, "down/merge launch");                      \
+    }
+    DIH_DM_CASE(8, 2) DIH_DM_CASE(8, 4) DIH_DM_CASE(8, 8) DIH_DM_CASE(8, 16) DIH_DM_CASE(8, 32) DIH_DM_CASE(8, 64)
+    DIH_DM_CASE(5, 2) DIH_DM_CASE(5, 4) DIH_DM_CASE(5, 8) DIH_DM_CASE(5, 16) DIH_DM_CASE(5, 32) DIH_DM_CASE(5, 64)
+#undef DIH_DM_CASE
+    set_error(error, capacity, "Unsupported down projection width");
+    return false;
 }
 
 // Full-matrix dequantization to bf16 (expanded_weights, prefill_bf16_expanded.mm:8-16):
@@ -341,9 +356,9 @@ bool launch_dequant_bf16(const Matrix *m, int expert, uint16_t *out, hipStream_t
     const uint16_t *sc = m->scales() + off * m->groups_per_row();
     const uint16_t *bi = m->biases() + off * m->groups_per_row();
     if (m->bits == 8)
-        hipLaunchKernelGGL((dequant_bf16_kernel<8>), grid, block, 0, s, p, sc, bi, m->rows, m->columns, out);
+        DIH_LAUNCH((dequant_bf16_kernel<8>), grid, block, 0, s, p, sc, bi, m->rows, m->columns, out);
     else
-        hipLaunchKernelGGL((dequant_bf16_kernel<5>), grid, block, 0, s, p, sc, bi, m->rows, m->columns, out);
+        DIH_LAUNCH((dequant_bf16_kernel<5>), grid, block, 0, s, p, sc, bi, m->rows, m->columns, out);
     return hip_ok(hipGetLastError(), error, capacity, "dequant launch");
 }
 
@@ -365,8 +380,8 @@ __global__ void embedding_kernel(const uint32_t *packed, const uint16_t *scales,
 
 bool launch_embedding(const Matrix *m, int token, float *out, hipStream_t s, char *error,
                       int capacity) {
-    hipLaunchKernelGGL(embedding_kernel, dim3((m->columns + 255) / 256), dim3(256), 0, s,
-                       m->packed(), m->scales(), m->biases(), m->bits, m->columns, token, out);
+    DIH_LAUNCH(embedding_kernel, dim3((m->columns + 255) / 256), dim3(256), 0, s, m->packed(), m->scales(),
+               m->biases(), m->bits, m->columns, token, out);
     return hip_ok(hipGetLastError(), error, capacity, "embedding launch");
 }
 

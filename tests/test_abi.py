@@ -1,0 +1,57 @@
+"""CPU checks of the C ABI library: it loads, exports exactly what include/deepinfer_hip.h
+declares, and fails loudly (no CPU fallback) where no gfx950 device is present."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import deepinfer_hip as dh
+
+HEADER = dh.HEADER_PATH
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dih_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built_and_loads():
+    assert os.path.exists(dh.LIB_PATH), "build with __graft_entry__.build()"
+    dh.load()
+
+
+def test_every_declared_entry_point_is_exported():
+    lib = ctypes.CDLL(dh.LIB_PATH)
+    names = declared()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(dh.EXPORTS) == names
+
+
+def test_only_declared_symbols_are_exported():
+    """The library hides its internals (-fvisibility=hidden): the dynamic symbol table holds
+    the dih_ entry points and nothing else of ours."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", dh.LIB_PATH], capture_output=True, text=True).stdout
+    ours = sorted({l.split()[-1] for l in out.splitlines() if " T " in l and "dih" in l})
+    assert ours == declared()
+
+
+def test_version_string():
+    assert "gfx950" in dh.version()
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd") and os.access("/dev/kfd", os.R_OK | os.W_OK),
+                    reason="a GPU node is present")
+def test_context_creation_fails_loudly_without_gpu():
+    with pytest.raises(dh.InvalidOperationError):
+        dh.QuantizedHip()
+
+
+def test_host_side_argument_validation_without_gpu():
+    """Validation that happens before any device call (QuantizedMetal.cs:14, 34-36)."""
+    with pytest.raises(dh.ArgumentOutOfRangeError):
+        dh.QuantizedHip(residency_refresh_milliseconds=60001)

@@ -352,14 +352,20 @@ def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
         assert np.max(np.abs(probs.cpu().numpy() - opr)) <= 1e-6
         xf = orc.bf16_bits_to_f32(xb)
         got_ro = rout.cpu().numpy()
-        # per-route down outputs against the oracle with the reference's bf16 operand
-        # rounding (weights, x, SwiGLU activation) and against the unrounded fp64 oracle
-        _, ro_bf = orc.moe_f64(L, xf, oid, opr, bf16_operands=True, route_out=True)
-        y, ro = orc.moe_f64(L, xf, oid, opr, bf16_operands=False, route_out=True)
-        e_bf, e_exact = orc.rel_err(got_ro, ro_bf), orc.rel_err(got_ro, ro)
-        assert e_bf < TOL and e_exact < TOL, (e_bf, e_exact)
+        # Per-route down outputs against the fp64 oracle of the reference's BF16 prefill
+        # path: dequantized weights, x and the SwiGLU activation rounded to bf16 (RNE) as
+        # packed_expert_load / expanded_pack do and as prefill_expert_checks.mm:56 models.
+        # (The GPU rounds its fp32 SwiGLU value to bf16, the oracle its fp64 value, so an
+        # activation can land one bf16 step apart; that moves outputs by ~1e-3 of RMS.)
+        y_bf, ro_bf = orc.moe_f64(L, xf, oid, opr, bf16_operands=True, route_out=True)
+        e_bf = orc.rel_err(got_ro, ro_bf)
+        assert e_bf < TOL, e_bf
+        # Against unrounded fp64 the difference is the bf16 operand rounding itself (a few
+        # 2^-9 relative steps at the extremes), the same for the reference's BF16 path.
+        _, ro = orc.moe_f64(L, xf, oid, opr, bf16_operands=False, route_out=True)
+        assert orc.rel_err(got_ro, ro) < 5e-2
         # residual = bf16(residual + sigmoid-gated shared + probability-weighted experts)
-        assert_rounded(host_bf16(res), orc.bf16_bits_to_f32(rb).astype(np.float64) + y, rms(y))
+        assert_rounded(host_bf16(res), orc.bf16_bits_to_f32(rb).astype(np.float64) + y_bf, rms(y_bf))
     finally:
         for m in q:
             if m is not None:

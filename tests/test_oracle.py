@@ -1,0 +1,280 @@
+"""CPU checks that pin the oracle (oracle/oracle.c via oracle/oracle.py).
+
+Each oracle function is checked against something it does not itself compute: the
+reference's own closed forms and known answers (QuantizedTests.cs, graph_checks.mm,
+prefill_expert_checks.mm, split_prefix.cu's self-test, ModelTests.cs), an independent
+numpy implementation (bit-string unpack, dense matmul), torch's bf16 conversion, or brute
+force. A planted-mistake test shows the unpack check rejects a wrong bit layout.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests import refcases
+
+
+# ------------------------------------------------------------ bf16 round-to-nearest-even
+
+def test_bf16_rne_matches_torch_and_known_values():
+    rng = np.random.default_rng(0)
+    v = np.concatenate([rng.normal(size=20000).astype(np.float32) * 10 ** rng.uniform(-6, 6, 20000).astype(np.float32),
+                        np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -1 - 2 ** -8, 0.0, -0.0, 65504.0], dtype=np.float32)])
+    ours = orc.f32_to_bf16_bits(v)
+    ref = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+    assert [int(orc.lib().orc_f32_to_bf16(float(x))) for x in (1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8)] == [0x3F80, 0x3F80, 0x3F82]
+    assert orc.lib().orc_bf16_to_f32(0x3B80) == 2 ** -8 and orc.lib().orc_bf16_to_f32(0xBE80) == -0.25
+
+
+# ---------------------------------------------------------------------- unpack + dequant
+
+@pytest.mark.parametrize("bits", [5, 8])
+def test_code_extraction_matches_independent_bitstring_unpack(bits):
+    rng = np.random.default_rng(bits)
+    words = rng.integers(0, 2 ** 32, size=(3, 7, 256 * bits // 32), dtype=np.uint64).astype(np.uint32)
+    want = orc.unpack_codes(words, bits, 256)
+    L = orc.lib()
+    for e in range(3):
+        for r in range(7):
+            row = np.ascontiguousarray(words[e, r])
+            got = [L.orc_code(row.ctypes.data, bits, c) for c in range(256)]
+            assert got == list(want[e, r])
+
+
+def test_planted_unpack_mistake_is_caught():
+    """A bit layout off by one position (MSB-first within each code) must not reproduce the
+    reference's closed form; the check below has teeth."""
+    m = refcases.populate(2, 5, 128, 5, 3)
+    words = m.packed.reshape(2, 5, -1)
+    codes = orc.unpack_codes(words, 5, 128)
+    wrong = np.zeros_like(codes)
+    for b in range(5):
+        wrong |= ((codes >> b) & 1) << (4 - b)
+    c = np.arange(128)[None, None, :]
+    e = np.arange(2)[:, None, None]
+    r = np.arange(5)[None, :, None]
+    closed = (c * 7 + e * 3 + r * 5 + 3 * 11) & 31
+    assert np.array_equal(codes, closed)
+    assert not np.array_equal(wrong, closed)
+
+
+@pytest.mark.parametrize("bits", [5, 8])
+@pytest.mark.parametrize("columns", [64, 192, 256, 512, 2048, 4096])
+def test_dequant_row_reproduces_reference_scalar_weight(bits, columns):
+    """Populate + ScalarWeight (QuantizedTests.cs:136-165): the packed matrix the reference's
+    test writes dequantizes, row by row, to exactly the closed-form float32 weights."""
+    m = refcases.populate(9, 5, columns, bits, 3)
+    want = refcases.scalar_weights(9, 5, columns, bits, 3)
+    out = np.zeros(columns, dtype=np.float32)
+    for e in (0, 4, 8):
+        for r in range(5):
+            orc.lib().orc_dequant_row(orc.ctypes.byref(m.c), e, r, out.ctypes.data)
+            assert np.array_equal(out, want[e, r])
+    assert np.array_equal(m.dequant(), want)
+
+
+# -------------------------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("bits", [5, 8])
+def test_qmv_selected_expert_closed_form(bits):
+    """SelectedExpertGemv (QuantizedTests.cs:228-256): scale 1.0, bias 0.5 =>
+    y = sum (q + .5) x exactly."""
+    e = np.arange(3)[:, None, None]
+    r = np.arange(7)[None, :, None]
+    c = np.arange(128)[None, None, :]
+    q = ((c * 7 + e * 3 + r) & ((1 << bits) - 1)).astype(np.uint32)
+    m = orc.QMatrix(orc.pack_codes(q, bits), np.full(42, 0x3F80, np.uint16), np.full(42, 0x3F00, np.uint16), 3, 7, 128, bits)
+    x = np.sin(np.arange(256, dtype=np.float32) * np.float32(.17)).astype(np.float32)
+    y = orc.qmv_f64(m, x, [2, 0], batched=True)
+    for slot, ex in enumerate([2, 0]):
+        want = (q[ex].astype(np.float64) + .5) @ x[slot * 128:(slot + 1) * 128].astype(np.float64)
+        assert np.max(np.abs(y[slot * 7:(slot + 1) * 7] - want)) < 1e-9
+
+
+def test_qmv_cuda_selftest_known_answer():
+    """di_cuda_prefix_selftest (split_prefix.cu:621-649): w=(i*17+3)%256, scale 0x3b80 (1/256),
+    bias 0xbe80 (-0.25) => y = sum (w/256 - .25) x; two experts selected [1, 0]."""
+    w = ((np.arange(2 * 13 * 256) * 17 + 3) % 256).astype(np.uint32).reshape(2, 13, 256)
+    m = orc.QMatrix(orc.pack_codes(w, 8), np.full(2 * 13 * 4, 0x3B80, np.uint16), np.full(2 * 13 * 4, 0xBE80, np.uint16),
+                    2, 13, 256, 8)
+    x = (((np.arange(256) * 11) % 23 - 11) / np.float32(23)).astype(np.float32)
+    y = orc.qmv_f64(m, x, [1, 0])
+    for s, e in enumerate([1, 0]):
+        want = (w[e].astype(np.float64) / 256 - .25) @ x.astype(np.float64)
+        assert np.max(np.abs(y[s * 13:(s + 1) * 13] - want)) < 1e-12
+
+
+def test_qmv_zero_codes_bias_only_closed_form():
+    """IndependentMixedGemvs (QuantizedTests.cs:166-209): zero codes, scale 1, bias b => b*sum(x)."""
+    m = orc.QMatrix(np.zeros(3 * 7 * 128 * 8 // 32, np.uint32), np.full(3 * 7 * 2, 0x3F80, np.uint16),
+                    orc.f32_to_bf16_bits((2 + (np.arange(42) // 2) * .25).astype(np.float32)), 3, 7, 128, 8)
+    x = ((np.arange(256) - 100) * np.float32(.005)).astype(np.float32)
+    y = orc.qmv_f64(m, x, [2, 0], batched=True)
+    for slot, e in enumerate([2, 0]):
+        for r in range(7):
+            want = (2 + (e * 7 + r) * .25) * x[slot * 128:(slot + 1) * 128].astype(np.float64).sum()
+            assert abs(y[slot * 7 + r] - want) < 1e-9
+
+
+@pytest.mark.parametrize("bits", [5, 8])
+def test_qmv_and_dense_match_numpy_matmul(bits):
+    rng = np.random.default_rng(11)
+    m = orc.random_matrix(rng, 4, 33, 320, bits)
+    W = m.dequant().astype(np.float64)
+    x = rng.normal(size=(6, 320)).astype(np.float32)
+    y = orc.qmv_f64(m, x[0], [3])
+    assert np.max(np.abs(y - W[3] @ x[0])) < 1e-9
+    d = orc.dense_f64(m, x, expert=2, round_operands=False)
+    assert np.max(np.abs(d - x.astype(np.float64) @ W[2].T)) < 1e-9
+    d_bf = orc.dense_f64(m, x, expert=2, round_operands=True)
+    want_bf = orc.round_bf16(x).astype(np.float64) @ orc.round_bf16(W[2].astype(np.float32)).astype(np.float64).T
+    assert np.max(np.abs(d_bf - want_bf)) < 1e-9
+
+
+def test_cpu_baseline_path_matches_fp64():
+    """The reference-faithful fp32 CPU path (MatVec.cs:40-55 after row dequant) agrees with the
+    fp64 oracle to fp32 accuracy, single- and multi-threaded (identical results)."""
+    rng = np.random.default_rng(12)
+    m = orc.random_matrix(rng, 3, 100, 2048, 8)
+    x = rng.normal(size=2048).astype(np.float32)
+    a = orc.cpu_qmv(m, x, [2, 1], threads=1)
+    b = orc.cpu_qmv(m, x, [2, 1], threads=4)
+    assert np.array_equal(a, b)
+    assert orc.rel_err(a, orc.qmv_f64(m, x, [2, 1])) < 1e-5
+
+
+# ------------------------------------------------------------------------------ routing
+
+def test_top8_reference_known_answers():
+    """graph_checks.mm:63-77 (stable-sort oracle, probability closed form) and the routing
+    KAT of QuantizedTests.cs:280-288."""
+    for v in refcases.top8_cases():
+        ids, probs = orc.top8(v)
+        exp = refcases.stable_top8(v)
+        assert np.array_equal(ids, exp)
+        ch = v[exp].astype(np.float64)
+        p = np.exp(ch - ch[0])
+        p /= p.sum()
+        assert np.max(np.abs(probs - p)) <= 1e-6
+    ids, probs = orc.top8((np.arange(256) * np.float32(.01)).astype(np.float32))
+    assert list(ids) == list(range(255, 247, -1))
+    assert abs(probs.sum() - 1) <= 1e-6 and probs[0] > probs[7]
+    with pytest.raises(ValueError):
+        orc.top8(np.where(np.arange(256) == 9, np.nan, 0).astype(np.float32))
+
+
+def test_top8_bf16_matches_brute_force_with_ties():
+    rng = np.random.default_rng(3)
+    lg = orc.round_bf16(rng.normal(size=(500, 256)).astype(np.float32))
+    lg[::5, 20:60] = 2.5
+    ids, _ = orc.top8_bf16(orc.f32_to_bf16_bits(lg))
+    for t in range(500):
+        assert np.array_equal(ids[t], refcases.stable_top8(lg[t]))
+
+
+@pytest.mark.parametrize("count", [64, 65, 127, 128, 129, 512, 513, 2048])
+@pytest.mark.parametrize("pattern", [0, 1, 2])
+def test_build_groups_invariants(count, pattern):
+    """prefill_expert_checks.mm:44-52: every route once, under its expert, counts; plus the
+    ascending order of prefill_build_groups' prefix sum (prefill_moe.mm:12-14)."""
+    ids = refcases.route_pattern(pattern, count)
+    counts, routes = orc.build_groups(ids, count, 256)
+    flat = ids.reshape(-1)
+    assert np.array_equal(counts, np.bincount(flat, minlength=256))
+    seen = np.zeros(count * 8, bool)
+    for e in range(256):
+        lst = routes[e * count:e * count + counts[e]]
+        assert np.array_equal(lst, np.flatnonzero(flat == e))
+        seen[lst] = True
+    assert seen.all()
+    tiles = sum((int(c) + 63) // 64 for c in counts)
+    assert tiles == sum(1 for e in range(256) for s in range(0, counts[e], 64))
+
+
+def test_argmax_known_answers():
+    """graph_checks.mm:89-103 and ModelTests.cs:23-28."""
+    base = (np.arange(248320, dtype=np.float32) * np.float32(1e-5)).astype(np.float32)
+    assert orc.argmax(base) == 248319
+    t = base.copy(); t[100] = t[200] = 10
+    assert orc.argmax(t) == 100
+    t = base.copy(); t[0] = np.nan
+    assert orc.argmax(t) == 0xFFFFFFFF
+    assert orc.argmax(np.array([1, 3, 3], np.float32)) == 1
+    assert orc.argmax(np.array([np.inf], np.float32)) == 0xFFFFFFFF
+
+
+# --------------------------------------------------------------------------- MoE blocks
+
+def _layer(rng, E, H, I, bits):
+    mk = lambda e, r, c, b=bits: orc.random_matrix(rng, e, r, c, b)  # noqa: E731
+    return orc.MoeLayer(orc.random_matrix(rng, 1, E, H, 8, 1.25e-4, 5e-4), mk(E, I, H), mk(E, I, H), mk(E, H, I),
+                        mk(1, I, H), mk(1, I, H), mk(1, H, I), orc.random_matrix(rng, 1, 1, H, 8))
+
+
+def _numpy_moe(L, x, ids, probs, rounded):
+    r = orc.round_bf16 if rounded else (lambda a: a)
+    W = {k: getattr(L, k).dequant().astype(np.float32) for k in ("gate", "up", "down", "shared_gate", "shared_up",
+                                                                "shared_down", "shared_route")}
+    if rounded:
+        for k in ("gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
+            W[k] = orc.round_bf16(W[k])
+    W = {k: v.astype(np.float64) for k, v in W.items()}
+    silu = lambda v: v / (1 + np.exp(-v))  # noqa: E731
+    y = np.zeros((x.shape[0], L.down.rows))
+    for t in range(x.shape[0]):
+        xt = r(x[t]).astype(np.float64)
+        sa = silu(W["shared_gate"][0] @ xt) * (W["shared_up"][0] @ xt)
+        sa = r(sa.astype(np.float32)).astype(np.float64) if rounded else sa
+        gate = 1 / (1 + np.exp(-(W["shared_route"][0, 0] @ x[t].astype(np.float64))))
+        y[t] = (W["shared_down"][0] @ sa) * gate
+        for s in range(8):
+            e = ids[t, s]
+            a = silu(W["gate"][e] @ xt) * (W["up"][e] @ xt)
+            a = r(a.astype(np.float32)).astype(np.float64) if rounded else a
+            y[t] += probs[t, s] * (W["down"][e] @ a)
+    return y
+
+
+@pytest.mark.parametrize("rounded", [False, True])
+def test_moe_f64_matches_numpy_composition(rounded):
+    """Moe (Qwen36Model.cs:218-245) / prefill merge order, against a numpy composition of
+    dense matmuls (independent of oracle.c's loops)."""
+    rng = np.random.default_rng(21)
+    L = _layer(rng, 16, 128, 64, 5)
+    x = orc.round_bf16(rng.normal(size=(5, 128)).astype(np.float32))
+    ids, probs = orc.top8_bf16(orc.f32_to_bf16_bits(rng.normal(size=(5, 16)).astype(np.float32)))
+    y = orc.moe_f64(L, x, ids, probs, bf16_operands=rounded)
+    want = _numpy_moe(L, x, ids, probs, rounded)
+    assert np.max(np.abs(y - want)) < 1e-6 * max(1.0, np.abs(want).max())
+
+
+def test_expert_mlp_matches_reference_closed_form():
+    """FusedExperts (QuantizedTests.cs:71-117) on the reference's closed-form weights."""
+    g, u = refcases.populate(9, 192, 128, 8, 1), refcases.populate(9, 192, 128, 8, 2)
+    d, s = refcases.populate(9, 128, 192, 5, 3), refcases.populate(1, 128, 64, 5, 4)
+    x = (np.sin(np.arange(128, dtype=np.float32) * np.float32(.13)) * np.float32(.1)).astype(np.float32)
+    sx = (np.cos(np.arange(64, dtype=np.float32) * np.float32(.07)) * np.float32(.2)).astype(np.float32)
+    ids = [8, 0, 6, 2, 5, 1, 7, 3]
+    out, sout = orc.expert_mlp_f64(g, u, d, s, x, sx, ids)
+    wg, wu = refcases.scalar_weights(9, 192, 128, 8, 1), refcases.scalar_weights(9, 192, 128, 8, 2)
+    wd, ws = refcases.scalar_weights(9, 128, 192, 5, 3), refcases.scalar_weights(1, 128, 64, 5, 4)
+    for slot, e in enumerate(ids):
+        gg = wg[e].astype(np.float64) @ x
+        uu = wu[e].astype(np.float64) @ x
+        act = gg / (1 + np.exp(-gg)) * uu
+        # ScalarWeight differs from the exact q*s+b by at most one fp32 rounding
+        assert np.max(np.abs(out[slot * 128:(slot + 1) * 128] - wd[e].astype(np.float64) @ act)) < 3e-6
+    assert np.max(np.abs(sout - ws[0].astype(np.float64) @ sx)) < 3e-6
+
+
+def test_cpu_moe_token_matches_fp64():
+    """The CPU baseline's MoE token (fp32, reference host order) against fp64."""
+    rng = np.random.default_rng(31)
+    L = _layer(rng, 32, 256, 128, 8)
+    x = orc.round_bf16(rng.normal(size=256).astype(np.float32))
+    y = orc.cpu_moe_token(L, x)
+    logits = orc.cpu_qmv(L.router, x)
+    ids, probs = orc.top8(logits)
+    want = orc.moe_f64(L, x[None, :], ids[None, :], probs[None, :], bf16_operands=False)[0]
+    assert orc.rel_err(y, want) < 1e-4

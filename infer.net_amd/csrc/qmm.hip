@@ -171,7 +171,8 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
                 v[k] = GATED ? siluf_(g) * acc1[t][4 * q + k] : g;
             }
             const size_t o = (size_t)route * R + m0;
-            if (m0 + 3 < R) {
+            // vector stores only where the row offset keeps them naturally aligned
+            if ((R & 3) == 0 && m0 + 3 < R) {
                 if (P.y_bf16) {
                     uint2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(P.y) + o) = pk;

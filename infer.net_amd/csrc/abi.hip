@@ -66,10 +66,12 @@ ProfScope::ProfScope(Context *c) {
 ProfScope::~ProfScope() { tl_prof_ctx = nullptr; }
 void prof_stage(const char *name) { tl_prof_name = name; }
 
-// Names the launches recorded since the previous mark (the kernels of one stage).
+// Names the launches recorded since the previous mark (the kernels of one stage) that
+// were not already named by prof_stage().
 static void prof_mark(Context *c, hipStream_t, const char *name) {
     if (!c->profiling || tl_prof_ctx != c) return;
-    for (size_t i = tl_prof_first; i < c->prof_recs.size(); i++) c->prof_recs[i].name = name;
+    for (size_t i = tl_prof_first; i < c->prof_recs.size(); i++)
+        if (strcmp(c->prof_recs[i].name, "kernel") == 0) c->prof_recs[i].name = name;
     tl_prof_first = c->prof_recs.size();
 }
 
@@ -720,6 +722,25 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
     if (!lg || !srt || !sact || !act || !sout || !ids || !probs || !tk || !status) return -1;
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);
+    if (decode_fast_path_ok(router, gate, down, sg, sd, sr)) {
+        float2 *cand = static_cast<float2 *>(scratch(c, S_CAND, 64 * sizeof(float2), error, capacity));
+        if (!cand) return -1;
+        DecodeLaunch a;
+        a.router = router; a.gate = gate; a.up = up; a.down = down;
+        a.shared_gate = sg; a.shared_up = su; a.shared_down = sd; a.shared_route = sr;
+        a.logits_in = logits;
+        a.logits = trace && trace->logits ? trace->logits : lg;
+        a.cand = cand; a.sact = sact; a.sroute = srt; a.act = act;
+        a.ids = trace && trace->ids ? trace->ids : ids;
+        a.probs = trace && trace->probs ? trace->probs : probs;
+        a.status = trace ? trace->status : nullptr;
+        a.x = static_cast<const uint16_t *>(x);
+        a.residual = static_cast<uint16_t *>(residual);
+        a.route_out = trace ? trace->expert_out : nullptr;
+        const bool ok = launch_moe_decode(a, s, error, capacity);
+        prof_stage("kernel");
+        return ok ? 0 : -1;
+    }
     const float *use_logits = logits ? logits : lg;
     // Stage 1: router logits, shared-expert gate GEMV and shared gate/up SwiGLU share x;
     // the last block of the launch that holds the router selects the experts.

@@ -1,0 +1,444 @@
+// Decode MoE step for one token in three launches (g_router, gpu_graph.mm:296-320, with
+// graph_top8 gpu_graph.mm:134-146 and graph_merge_norm gpu_graph.mm:48-61; host form
+// Qwen36Model.cs:218-245):
+//
+//   K1 router/shared  : router logits in 32-expert chunks; each chunk block ranks its 32
+//                       logits in LDS and writes its top-8 as candidates (value, id).
+//                       The same launch computes the shared expert's gate/up SwiGLU and the
+//                       shared-expert sigmoid gate row.
+//   K2 experts gate/up: every wave merges the <= 64 candidates by rank (the top-8 of the
+//                       union of per-chunk top-8s is the global top-8, ties to the lowest
+//                       id) and streams four gated rows of its slot's expert.
+//   K3 down + merge   : blocks of nine waves; waves 0..7 compute the selected experts'
+//                       down rows for the block's output rows, wave 8 the shared expert's;
+//                       the merge y = sigmoid(route)*shared + sum_slot p_slot*expert_slot
+//                       (slot order 0..7) and residual = bf16(residual + y) happen in LDS.
+//
+// Kernel boundaries are the only cross-block synchronization: on MI355X a device-scope
+// counter or flag shared by hundreds of blocks costs more than a launch. Every wave issues
+// all of its weight loads before it waits on any of them; scale/bias words stay raw until
+// they are consumed.
+#include "dih_device.h"
+#include "dih_internal.h"
+
+namespace dih {
+
+namespace {
+
+constexpr int kChunkExperts = 32;  // experts per router block
+constexpr int kWaves = 16;         // waves per K1/K2 block
+constexpr int kRouterGroups = 2;   // K1 router: row groups per wave (32 rows per block)
+constexpr int kDownGroups = 2;     // K3: row groups per wave
+
+// One lane's share of NG row groups of one matrix.
+template <int BITS, int NG>
+struct Rows {
+    Chunk<BITS> w[NG];
+    uint32_t s[NG], b[NG];
+};
+
+// Row of group q for this lane: row0 + q*rpw + g, clamped into [0, nrows).
+template <int BITS, int NG>
+DIH_DEV void rows_load(Rows<BITS, NG> &R, const uint32_t *p, const uint16_t *sc, const uint16_t *bi,
+                       size_t rowbase, int nrows, int row0, int rpw, int g, int jc, int columns) {
+    const size_t wpr = (size_t)columns * BITS / 32, gpr = (size_t)(columns >> 6);
+#pragma unroll
+    for (int q = 0; q < NG; q++) {
+        int r = row0 + q * rpw + g;
+        r = r < nrows ? r : nrows - 1;
+        const size_t ri = rowbase + r;
+        load_chunk<BITS>(R.w[q], p + ri * wpr, jc);
+        R.s[q] = sc[ri * gpr + (jc >> 1)];
+        R.b[q] = bi[ri * gpr + (jc >> 1)];
+    }
+}
+
+// Per-lane partial dot of group q (masked lanes contribute 0), then the row sum over
+// the lpr lanes of the row.
+template <int BITS, int NG>
+DIH_DEV void rows_dot(const Rows<BITS, NG> &R, const float (&x)[32], float xs, bool valid, int lpr,
+                      float (&out)[NG]) {
+#pragma unroll
+    for (int q = 0; q < NG; q++) {
+        float v = bf16_to_f32(R.s[q]) * chunk_dot<BITS>(R.w[q], x) + bf16_to_f32(R.b[q]) * xs;
+        out[q] = group_sum(valid ? v : 0.f, lpr);
+    }
+}
+
+// Lane geometry of a row of `columns` codes: lpr lanes per row, this lane's chunk.
+struct LaneGeom {
+    int lpr, rpw, g, j, jc;
+    bool valid;
+};
+DIH_DEV LaneGeom lane_geom(int columns, int lpr) {
+    LaneGeom L;
+    const int lane = threadIdx.x & 63, nchunk = columns >> 5;
+    L.lpr = lpr;
+    L.rpw = 64 / lpr;
+    L.g = lane / lpr;
+    L.j = lane - L.g * lpr;
+    L.valid = L.j < nchunk;
+    L.jc = L.valid ? L.j : nchunk - 1;
+    return L;
+}
+
+// Activations staged once per block in LDS as f32, plus their 32-column sums. Element i
+// of chunk c sits at c*32 + ((i + 4*(c & 7)) & 31): a lane reading its chunk as eight
+// 16-byte pieces then hits a different bank quad than its seven neighbours.
+DIH_DEV int xl_at(int c, int i) { return c * 32 + ((i + 4 * (c & 7)) & 31); }
+
+// Raw bf16 activations of this thread's eight columns (issued before the weights so that
+// waiting for them does not wait for the weight stream).
+DIH_DEV uint4 stage_x_load(const uint16_t *x, int H) {
+    const int t = threadIdx.x;
+    return t < (H >> 3) ? reinterpret_cast<const uint4 *>(x)[t] : make_uint4(0, 0, 0, 0);
+}
+
+DIH_DEV void stage_x_store(const uint4 v, int H, float *xl, float *xsl) {
+    const int t = threadIdx.x;
+    if (t < (H >> 3)) {
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        float f[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            f[2 * k] = __uint_as_float(u[k] << 16);
+            f[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+        }
+        const int c = t >> 2, i0 = (t & 3) * 8;
+        *reinterpret_cast<float4 *>(&xl[xl_at(c, i0)]) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4 *>(&xl[xl_at(c, i0 + 4)]) = make_float4(f[4], f[5], f[6], f[7]);
+        float sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+        sum += dppf<DIH_DPP_XOR1>(sum);
+        sum += dppf<DIH_DPP_XOR2>(sum);
+        if ((t & 3) == 0) xsl[c] = sum;
+    }
+}
+
+// This lane's 32 activations from the staged copy, and their sum.
+DIH_DEV float lane_x_lds(float (&x)[32], const float *xl, const float *xsl, const LaneGeom &L) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const float4 v = *reinterpret_cast<const float4 *>(&xl[xl_at(L.jc, 4 * q)]);
+        x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    }
+    return xsl[L.jc];
+}
+
+// Activations of this lane's chunk as f32 straight from global memory, and their sum.
+DIH_DEV float lane_x(float (&x)[32], const void *base, int x_bf16, const LaneGeom &L) {
+    load_x32(x, base, x_bf16, L.jc * 32);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) s += x[i];
+    return s;
+}
+
+// (value desc, id asc): does candidate (va, ia) come before (vb, ib)?
+DIH_DEV bool before(float va, uint32_t ia, float vb, uint32_t ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+
+}  // namespace
+
+struct DecodeParams {
+    const uint32_t *rp; const uint16_t *rs, *rb;           // router [E, H], 8-bit (or null)
+    const float *logits_in;                                 // supplied logits [E] (router null)
+    float *logits;                                          // router logits out [E]
+    float2 *cand;                                           // [nchunks * 8] (value, id bits)
+    const uint32_t *sgp, *sup; const uint16_t *sgs, *sgb, *sus, *sub;  // shared gate/up [I, H]
+    const uint32_t *srp; const uint16_t *srs, *srb;         // shared route [1, H], 8-bit
+    float *sact;                                            // [I]
+    float *sroute;                                          // [1]
+    const uint32_t *gp, *upp; const uint16_t *gs, *gb, *us, *ub;  // experts gate/up [E, I, H]
+    const uint32_t *dp; const uint16_t *ds, *db;            // experts down [E, H, I]
+    const uint32_t *sdp; const uint16_t *sds, *sdb;         // shared down [1, H, I]
+    float *act;                                             // [8, I]
+    uint32_t *ids; float *probs; uint32_t *status;          // published by K2
+    const uint16_t *x;                                      // bf16 [H]
+    uint16_t *residual;                                     // bf16 [H]
+    float *route_out;                                       // optional [9, H]
+    int E, H, I;
+    int lpr_h, lpr_i;
+    int nchunks;          // router blocks (ceil(E / 32))
+    int shared_blocks;    // K1 blocks for the shared gate/up
+    int gate_blocks;      // K2 blocks per slot
+    int down_rows;        // K3 output rows per block
+};
+
+// ------------------------------------------------------------------------------- K1
+
+template <int BITS>
+__global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
+    __shared__ __align__(16) float xl[2048];
+    __shared__ float xsl[64];
+    __shared__ __align__(16) float lg[kChunkExperts];
+    const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const LaneGeom L = lane_geom(P.H, P.lpr_h);
+    if (b < P.nchunks) {
+        // router rows b*32 + wave*2*rpw + q*rpw + g (8-bit); rows past the chunk are masked
+        const int wrow = wave * kRouterGroups * L.rpw;
+        const int base = b * kChunkExperts + wrow;
+        const int n = min(kChunkExperts, P.E - b * kChunkExperts);
+        if (P.rp) {
+            const uint4 xv = stage_x_load(P.x, P.H);
+            Rows<8, kRouterGroups> R;
+            rows_load<8, kRouterGroups>(R, P.rp, P.rs, P.rb, 0, P.E, base, L.rpw, L.g, L.jc, P.H);
+            stage_x_store(xv, P.H, xl, xsl);
+            __syncthreads();
+            float x[32];
+            const float xs = lane_x_lds(x, xl, xsl, L);
+            float v[kRouterGroups];
+            rows_dot<8, kRouterGroups>(R, x, xs, L.valid, L.lpr, v);
+#pragma unroll
+            for (int q = 0; q < kRouterGroups; q++) {
+                const int o = wrow + q * L.rpw + L.g;  // row within the chunk
+                if (L.j == 0 && o < n) {
+                    lg[o] = v[q];
+                    P.logits[b * kChunkExperts + o] = v[q];
+                }
+            }
+        } else if (threadIdx.x < kChunkExperts) {
+            const int e = b * kChunkExperts + threadIdx.x;
+            if ((int)threadIdx.x < n) {
+                lg[threadIdx.x] = P.logits_in[e];
+                P.logits[e] = P.logits_in[e];
+            }
+        }
+        // entries past the last expert rank after every real one
+        if (threadIdx.x < kChunkExperts && (int)threadIdx.x >= n) lg[threadIdx.x] = -INFINITY;
+        __syncthreads();
+        if (wave == 0) {
+            // rank of each of the chunk's logits (all LDS reads independent broadcasts);
+            // the eight first become candidates
+            const bool mine = lane < n;
+            const float v = lane < kChunkExperts ? lg[lane] : -INFINITY;
+            const uint32_t id = mine ? (uint32_t)(b * kChunkExperts + lane) : 0xffffff00u + (uint32_t)lane;
+            const bool bad = __any(mine && !isfinite(v));
+            int rank = 0;
+#pragma unroll
+            for (int k = 0; k < kChunkExperts; k += 4) {
+                const float4 q = *reinterpret_cast<const float4 *>(&lg[k]);
+                const float qv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t ik = k + i < n ? (uint32_t)(b * kChunkExperts + k + i) : 0xffffff00u + (uint32_t)(k + i);
+                    rank += before(qv[i], ik, v, id) ? 1 : 0;
+                }
+            }
+            if (lane < kChunkExperts && rank < 8)
+                P.cand[b * 8 + rank] = make_float2(v, __uint_as_float(bad ? 0xfffffffeu : id));
+        }
+        return;
+    }
+    const int sb = b - P.nchunks;
+    if (sb < P.shared_blocks) {
+        // shared expert gate/up SwiGLU: one row group (rpw rows) per wave
+        const int base = (sb * kWaves + wave) * L.rpw;
+        const uint4 xv = stage_x_load(P.x, P.H);
+        Rows<BITS, 1> G, U;
+        rows_load<BITS, 1>(G, P.sgp, P.sgs, P.sgb, 0, P.I, base, L.rpw, L.g, L.jc, P.H);
+        rows_load<BITS, 1>(U, P.sup, P.sus, P.sub, 0, P.I, base, L.rpw, L.g, L.jc, P.H);
+        stage_x_store(xv, P.H, xl, xsl);
+        __syncthreads();
+        float x[32];
+        const float xs = lane_x_lds(x, xl, xsl, L);
+        float a[1], c[1];
+        rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
+        rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, c);
+        if (L.j == 0 && base + L.g < P.I) P.sact[base + L.g] = siluf_(a[0]) * c[0];
+        return;
+    }
+    // shared-expert gate row (sigmoid applied at the merge)
+    if (wave == 0) {
+        Rows<8, 1> R;
+        rows_load<8, 1>(R, P.srp, P.srs, P.srb, 0, 1, 0, L.rpw, 0, L.jc, P.H);
+        float x[32];
+        const float xs = lane_x(x, P.x, 1, L);
+        float v[1];
+        rows_dot<8, 1>(R, x, xs, L.valid && L.g == 0, 64, v);
+        if (lane == 0) P.sroute[0] = v[0];
+    }
+}
+
+// ------------------------------------------------------------------------------- K2
+
+template <int BITS>
+__global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
+    __shared__ __align__(16) float xl[2048];
+    __shared__ float xsl[64];
+    __shared__ __align__(16) float2 cl[64];
+    __shared__ int rk[64];
+    __shared__ uint32_t chosen[8];
+    __shared__ float chosen_v[8];
+    __shared__ int any_bad;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int slot = blockIdx.x / P.gate_blocks;
+    const LaneGeom L = lane_geom(P.H, P.lpr_h);
+    const int base = ((blockIdx.x - slot * P.gate_blocks) * kWaves + wave) * L.rpw;
+    // candidates -> rank -> this slot's expert, ranked once per block: thread t compares
+    // candidate t%64 with the four candidates of sixteenth t/64 (slots past nc hold
+    // (-inf, 0xffffffff), which no candidate ranks behind)
+    const int nc = P.nchunks * 8;
+    if (t < 64) {
+        cl[t] = t < nc ? P.cand[t] : make_float2(-INFINITY, __uint_as_float(0xffffffffu));
+        rk[t] = 0;
+        if (t == 0) any_bad = 0;
+    }
+    stage_x_store(stage_x_load(P.x, P.H), P.H, xl, xsl);
+    __syncthreads();
+    {
+        const float2 me = cl[lane];
+        const uint32_t mid = __float_as_uint(me.y);
+        const float4 q0 = *reinterpret_cast<const float4 *>(&cl[wave * 4]);
+        const float4 q1 = *reinterpret_cast<const float4 *>(&cl[wave * 4 + 2]);
+        int r = before(q0.x, __float_as_uint(q0.y), me.x, mid) ? 1 : 0;
+        r += before(q0.z, __float_as_uint(q0.w), me.x, mid) ? 1 : 0;
+        r += before(q1.x, __float_as_uint(q1.y), me.x, mid) ? 1 : 0;
+        r += before(q1.z, __float_as_uint(q1.w), me.x, mid) ? 1 : 0;
+        if (r) atomicAdd(&rk[lane], r);
+        if (wave == 0 && lane < nc && mid == 0xfffffffeu) any_bad = 1;
+    }
+    __syncthreads();
+    if (t < nc && rk[t] < 8) {
+        chosen[rk[t]] = __float_as_uint(cl[t].y);
+        chosen_v[rk[t]] = cl[t].x;
+    }
+    __syncthreads();
+    const bool bad = any_bad != 0;
+    const uint32_t e = bad ? 0u : chosen[slot];
+    // one gated row group of expert e per wave
+    const size_t ebase = (size_t)e * P.I;
+    Rows<BITS, 1> G, U;
+    rows_load<BITS, 1>(G, P.gp, P.gs, P.gb, ebase, P.I, base, L.rpw, L.g, L.jc, P.H);
+    rows_load<BITS, 1>(U, P.upp, P.us, P.ub, ebase, P.I, base, L.rpw, L.g, L.jc, P.H);
+    if (blockIdx.x == 0 && t == 0) {
+        // softmax over the eight chosen logits, the first (largest) subtracted, summed in
+        // slot order (Softmax Qwen36Model.cs:293-298)
+        float p[8], total = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; s++) { p[s] = __expf(chosen_v[s] - chosen_v[0]); total += p[s]; }
+#pragma unroll
+        for (int s = 0; s < 8; s++) { P.ids[s] = bad ? 0u : chosen[s]; P.probs[s] = p[s] / total; }
+        if (bad && P.status) *P.status = 1u;
+    }
+    float x[32];
+    const float xs = lane_x_lds(x, xl, xsl, L);
+    float a[1], u[1];
+    rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
+    rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, u);
+    if (L.j == 0 && base + L.g < P.I) P.act[(size_t)slot * P.I + base + L.g] = siluf_(a[0]) * u[0];
+}
+
+// ------------------------------------------------------------------------------- K3
+
+template <int BITS>
+__global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
+    __shared__ float part[9][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = blockIdx.x * P.down_rows;
+    const LaneGeom L = lane_geom(P.I, P.lpr_i);
+    // merge operands first (wave 0 lanes < down_rows merge)
+    float res = 0.f, route = 0.f, pr[8];
+    const int h = row0 + lane;
+    if (wave == 0) {
+        route = P.sroute[0];
+#pragma unroll
+        for (int s = 0; s < 8; s++) pr[s] = P.probs[s];
+        if (lane < P.down_rows && h < P.H) res = bf16_to_f32(P.residual[h]);
+    }
+    const bool shared = wave == 8;
+    // activations first, then the expert id, then the weights that depend on it
+    float x[32];
+    const float *xa = shared ? P.sact : P.act + (size_t)wave * P.I;
+    load_x32(x, xa, 0, L.jc * 32);
+    const uint32_t e = shared ? 0u : P.ids[wave];
+    const uint32_t *wp = shared ? P.sdp : P.dp;
+    const uint16_t *ws = shared ? P.sds : P.ds, *wb = shared ? P.sdb : P.db;
+    Rows<BITS, kDownGroups> R;
+    rows_load<BITS, kDownGroups>(R, wp, ws, wb, (size_t)e * P.H, P.H, row0, L.rpw, L.g, L.jc, P.I);
+    float xs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) xs += x[i];
+    float v[kDownGroups];
+    rows_dot<BITS, kDownGroups>(R, x, xs, L.valid, L.lpr, v);
+#pragma unroll
+    for (int q = 0; q < kDownGroups; q++)
+        if (L.j == 0) part[wave][q * L.rpw + L.g] = v[q];
+    __syncthreads();
+    if (wave == 0 && lane < P.down_rows && h < P.H) {
+        const float sh = part[8][lane];
+        float y = sh * sigmoidf_(route);
+#pragma unroll
+        for (int s = 0; s < 8; s++) y += part[s][lane] * pr[s];
+        P.residual[h] = f32_to_bf16(res + y);
+        if (P.route_out) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) P.route_out[(size_t)s * P.H + h] = part[s][lane];
+            P.route_out[(size_t)8 * P.H + h] = sh;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------- host
+
+static int pow2ceil_(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix *down, const Matrix *sg,
+                         const Matrix *sd, const Matrix *sr) {
+    const int E = gate->experts, H = gate->columns, I = gate->rows;
+    return (!router || router->bits == 8) && sr->bits == 8 && sg->bits == gate->bits &&
+           sd->bits == gate->bits && down->bits == gate->bits && sg->rows == I && sd->columns == I &&
+           H <= 2048 && I <= 2048 && E <= 256 && (gate->bits == 8 || gate->bits == 5);
+}
+
+bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int capacity) {
+    DecodeParams P{};
+    const Matrix *gate = a.gate;
+    P.E = gate->experts; P.H = gate->columns; P.I = gate->rows;
+    P.lpr_h = std::min(64, pow2ceil_(P.H / 32));
+    P.lpr_i = std::min(64, pow2ceil_(P.I / 32));
+    if (a.router) { P.rp = a.router->packed(); P.rs = a.router->scales(); P.rb = a.router->biases(); }
+    P.logits_in = a.logits_in;
+    P.logits = a.logits;
+    P.cand = a.cand;
+    P.sgp = a.shared_gate->packed(); P.sgs = a.shared_gate->scales(); P.sgb = a.shared_gate->biases();
+    P.sup = a.shared_up->packed(); P.sus = a.shared_up->scales(); P.sub = a.shared_up->biases();
+    P.srp = a.shared_route->packed(); P.srs = a.shared_route->scales(); P.srb = a.shared_route->biases();
+    P.sact = a.sact; P.sroute = a.sroute;
+    P.gp = gate->packed(); P.gs = gate->scales(); P.gb = gate->biases();
+    P.upp = a.up->packed(); P.us = a.up->scales(); P.ub = a.up->biases();
+    P.dp = a.down->packed(); P.ds = a.down->scales(); P.db = a.down->biases();
+    P.sdp = a.shared_down->packed(); P.sds = a.shared_down->scales(); P.sdb = a.shared_down->biases();
+    P.act = a.act; P.ids = a.ids; P.probs = a.probs; P.status = a.status;
+    P.x = a.x; P.residual = a.residual; P.route_out = a.route_out;
+    P.nchunks = (P.E + kChunkExperts - 1) / kChunkExperts;
+    const int rows_per_block = kWaves * (64 / P.lpr_h);
+    P.shared_blocks = (P.I + rows_per_block - 1) / rows_per_block;
+    P.gate_blocks = P.shared_blocks;
+    P.down_rows = std::min(64, kDownGroups * (64 / P.lpr_i));
+    const int k1 = P.nchunks + P.shared_blocks + 1;
+    const int k2 = 8 * P.gate_blocks;
+    const int k3 = (P.H + P.down_rows - 1) / P.down_rows;
+    if (gate->bits == 8) {
+        prof_stage("decode_router_shared");
+        DIH_LAUNCH(decode_router_kernel<8>, dim3(k1), dim3(1024), 0, s, P);
+        prof_stage("decode_experts_gate_up");
+        DIH_LAUNCH(decode_experts_kernel<8>, dim3(k2), dim3(1024), 0, s, P);
+        prof_stage("decode_down_merge");
+        DIH_LAUNCH(decode_down_kernel<8>, dim3(k3), dim3(576), 0, s, P);
+    } else {
+        prof_stage("decode_router_shared");
+        DIH_LAUNCH(decode_router_kernel<5>, dim3(k1), dim3(1024), 0, s, P);
+        prof_stage("decode_experts_gate_up");
+        DIH_LAUNCH(decode_experts_kernel<5>, dim3(k2), dim3(1024), 0, s, P);
+        prof_stage("decode_down_merge");
+        DIH_LAUNCH(decode_down_kernel<5>, dim3(k3), dim3(576), 0, s, P);
+    }
+    return hip_ok(hipGetLastError(), error, capacity, "decode MoE launch");
+}
+
+}  // namespace dih

@@ -60,7 +60,7 @@ struct Context {
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_TICKETS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_CAND, S_COUNT_
 };
 
 // Error helpers (bridge.mm:9-15 convention).
@@ -153,6 +153,28 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity);
 bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens, int hidden,
                       const float *route_out, const float *probs, uint16_t *residual,
                       hipStream_t s, char *error, int capacity);
+
+// Decode MoE step in three launches (decode.hip). Device buffers: logits [E], cand
+// [ceil(E/32)*8] float2, sact [I], sroute [1], act [8*I], ids [8], probs [8], status [1]
+// (may be null), route_out [9*H] (may be null).
+struct DecodeLaunch {
+    const Matrix *router = nullptr, *gate = nullptr, *up = nullptr, *down = nullptr;
+    const Matrix *shared_gate = nullptr, *shared_up = nullptr, *shared_down = nullptr;
+    const Matrix *shared_route = nullptr;
+    const float *logits_in = nullptr;
+    float *logits = nullptr;
+    float2 *cand = nullptr;
+    float *sact = nullptr, *sroute = nullptr, *act = nullptr;
+    uint32_t *ids = nullptr;
+    float *probs = nullptr;
+    uint32_t *status = nullptr;
+    const uint16_t *x = nullptr;
+    uint16_t *residual = nullptr;
+    float *route_out = nullptr;
+};
+bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix *down, const Matrix *sg,
+                         const Matrix *sd, const Matrix *sr);
+bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int capacity);
 
 bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
                    uint32_t *ticket, uint32_t *next, hipStream_t s, char *error, int capacity);

@@ -8,36 +8,135 @@
 // once per lane per launch. This is the semantics of quant_rows / quant_dot
 // (quantized.mm:83-144) and expert_gate_up (quantized.mm:148-189), re-tiled for wave64.
 //
-// Latency: each wave walks its row groups (strided by the number of waves of the slot, so
-// the chip reads one contiguous region at a time) with two stages of kU row groups in
-// flight: the weights of stage t+1 are requested before stage t is reduced. The grid is
-// sized to about four blocks per CU so every wave is resident from the start. Weight loads
-// are issued before the activation loads and nothing waits on a cross-block fence.
+// Latency hiding: each wave keeps D row groups in flight in a register ring. The raw
+// words of a row group (codes and the bf16 bit patterns of its scales and biases) stay
+// untouched until the group is consumed, and every load is unconditional (row and chunk
+// indices are clamped in bounds, out-of-range lanes are masked at the reduction), so the
+// only wait before consuming ring slot d is for the loads issued before it: the D-1 later
+// groups stay in flight. Waves walk their row groups strided by the number of waves of
+// the slot, so the chip reads one contiguous region at a time.
 #include "dih_device.h"
 #include "dih_internal.h"
 
 namespace dih {
 
 constexpr int kMaxSeg = 4;
-constexpr int kU = 2;              // row groups per pipeline stage
-constexpr int kBlocksTarget = 1024;  // ~4 blocks of 256 threads per CU on 256 CUs
+constexpr int kWavesTarget = 4096;   // 16 resident waves per CU on 256 CUs
 
 struct QmvParams {
     QmvSeg seg[kMaxSeg];
     int start[kMaxSeg + 1];  // first block of each segment
     int lpr[kMaxSeg];
     int blocks_per_slot[kMaxSeg];
+    int waves_per_slot[kMaxSeg];
+    int iters[kMaxSeg];      // row groups per wave
     int nseg;
     Top8Source top8;
 };
 
-template <int BITS, int CPL>
-struct Stage {
-    Chunk<BITS> w[kU][CPL], u[kU][CPL];
-    float s[kU][CPL], b[kU][CPL], su[kU][CPL], bu[kU][CPL];
+// Raw words of one row group for one lane.
+template <int BITS, int CPL, bool GATED>
+struct RawGroup {
+    Chunk<BITS> w[CPL];
+    Chunk<BITS> u[GATED ? CPL : 1];
+    uint32_t s[CPL], b[CPL];
+    uint32_t su[GATED ? CPL : 1], bu[GATED ? CPL : 1];
 };
 
-template <int BITS, int CPL>
+template <int BITS, int CPL, bool GATED, int D>
+DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_id, int wi, int W,
+                      int K) {
+    const int lane = threadIdx.x & 63;
+    const int rpw = 64 / lpr;  // rows per row group
+    const int g = lane / lpr, j = lane - g * lpr;
+    const int nchunk = S.columns >> 5;
+    const size_t wpr = (size_t)S.columns * BITS / 32, gpr = (size_t)(S.columns >> 6);
+    const size_t ebase = (size_t)e * S.rows;
+    int chc[CPL];
+    bool valid[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        const int ch = j + c * lpr;
+        valid[c] = ch < nchunk;
+        chc[c] = valid[c] ? ch : nchunk - 1;
+    }
+
+    auto load = [&](RawGroup<BITS, CPL, GATED> &st, int grp) {
+        int r = grp * rpw + g;
+        r = r < S.rows ? r : S.rows - 1;
+        const size_t rowi = ebase + r;
+        const uint32_t *wrow = S.p0 + rowi * wpr;
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            load_chunk<BITS>(st.w[c], wrow, chc[c]);
+            st.s[c] = S.s0[rowi * gpr + (chc[c] >> 1)];
+            st.b[c] = S.b0[rowi * gpr + (chc[c] >> 1)];
+            if constexpr (GATED) {
+                load_chunk<BITS>(st.u[c], S.p1 + rowi * wpr, chc[c]);
+                st.su[c] = S.s1[rowi * gpr + (chc[c] >> 1)];
+                st.bu[c] = S.b1[rowi * gpr + (chc[c] >> 1)];
+            }
+        }
+    };
+
+    RawGroup<BITS, CPL, GATED> ring[D];
+#pragma unroll
+    for (int d = 0; d < D; d++) load(ring[d], wi + d * W);
+
+    // This lane's activations and their chunk sums (zero for masked chunks).
+    float xr[CPL][32];
+    float xs[CPL];
+    const void *xb = S.x_bf16
+        ? (const void *)(static_cast<const uint16_t *>(S.x) + (size_t)slot * S.x_slot_stride)
+        : (const void *)(static_cast<const float *>(S.x) + (size_t)slot * S.x_slot_stride);
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        load_x32(xr[c], xb, S.x_bf16, chc[c] * 32);
+        xs[c] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            xr[c][i] = valid[c] ? xr[c][i] : 0.f;
+            xs[c] += xr[c][i];
+        }
+    }
+
+    auto consume = [&](const RawGroup<BITS, CPL, GATED> &st, int grp) {
+        const int r = grp * rpw + g;
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            const float v = bf16_to_f32(st.s[c]) * chunk_dot<BITS>(st.w[c], xr[c]) + bf16_to_f32(st.b[c]) * xs[c];
+            a += valid[c] ? v : 0.f;
+            if constexpr (GATED) {
+                const float vu = bf16_to_f32(st.su[c]) * chunk_dot<BITS>(st.u[c], xr[c]) + bf16_to_f32(st.bu[c]) * xs[c];
+                b += valid[c] ? vu : 0.f;
+            }
+        }
+        a = group_sum(a, lpr);
+        if constexpr (GATED) b = group_sum(b, lpr);
+        if (j == 0 && r < S.rows) {
+            float v = a;
+            if constexpr (GATED) v = siluf_(a) * b;
+            if (bad_id) v = __builtin_nanf("");
+            const size_t o = (size_t)slot * S.rows + r;
+            if (S.y_bf16)
+                static_cast<uint16_t *>(S.y)[o] = f32_to_bf16(v);
+            else
+                static_cast<float *>(S.y)[o] = v;
+        }
+    };
+
+    for (int k0 = 0; k0 < K; k0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            consume(ring[d], wi + (k0 + d) * W);
+            // refill with the group D iterations ahead (clamped in bounds past the end)
+            if (D > 1 || k0 + D < K) load(ring[d], wi + (k0 + d + D) * W);
+        }
+    }
+}
+
+template <int BITS, int CPL, int D>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     const int blk = blockIdx.x;
     int k = 0;
@@ -45,15 +144,12 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     for (int i = 1; i < kMaxSeg; i++)
         if (i < P.nseg && blk >= P.start[i]) k = i;
     const QmvSeg &S = P.seg[k];
-    const int lpr = P.lpr[k];
     const int local = blk - P.start[k];
     const int slot = local / P.blocks_per_slot[k];
-    const int rb = local - slot * P.blocks_per_slot[k];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rpw = 64 / lpr;  // rows per row group
-    const int g = lane / lpr, j = lane - g * lpr;
-    const int nchunk = S.columns >> 5;
-    const bool gated = S.p1 != nullptr;
+    const int wi = (local - slot * P.blocks_per_slot[k]) * 4 + (threadIdx.x >> 6);
+    const int W = P.waves_per_slot[k];
+    if (wi >= W) return;
+    const int lane = threadIdx.x & 63;
 
     // Expert of this slot: a device id, or top-8 of the router logits computed by this
     // wave (the first wave of the segment publishes ids/probs for the next kernel).
@@ -66,7 +162,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
 #pragma unroll
         for (int q = 0; q < 8; q++)
             if (q == slot) e = ids[q];
-        if (local == 0 && wave == 0 && lane < 8) {
+        if (local == 0 && threadIdx.x < 8) {
 #pragma unroll
             for (int q = 0; q < 8; q++)
                 if (q == lane) { P.top8.ids[q] = ids[q]; P.top8.probs[q] = probs[q]; }
@@ -77,96 +173,10 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     }
     const bool bad_id = e >= (uint32_t)S.experts;
     if (bad_id) e = 0u;
-    const size_t wpr = (size_t)S.columns * BITS / 32, gpr = (size_t)(S.columns >> 6);
-    const size_t ebase = (size_t)e * S.rows;
-
-    const int groups_total = (S.rows + rpw - 1) / rpw;
-    const int W = P.blocks_per_slot[k] * 4;
-    const int wi = rb * 4 + wave;
-    const int stride = W * kU;
-    const int iters = wi < groups_total ? (groups_total - wi + stride - 1) / stride : 0;
-
-    auto load = [&](Stage<BITS, CPL> &st, int it) {
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            int r = (wi + (it * kU + u) * W) * rpw + g;
-            r = r < S.rows ? r : S.rows - 1;
-            const size_t rowi = ebase + r;
-            const uint32_t *wrow = S.p0 + rowi * wpr;
-#pragma unroll
-            for (int c = 0; c < CPL; c++) {
-                const int ch = j + c * lpr;
-                if (ch < nchunk) {
-                    load_chunk<BITS>(st.w[u][c], wrow, ch);
-                    st.s[u][c] = bf16_to_f32(S.s0[rowi * gpr + (ch >> 1)]);
-                    st.b[u][c] = bf16_to_f32(S.b0[rowi * gpr + (ch >> 1)]);
-                    if (gated) {
-                        load_chunk<BITS>(st.u[u][c], S.p1 + rowi * wpr, ch);
-                        st.su[u][c] = bf16_to_f32(S.s1[rowi * gpr + (ch >> 1)]);
-                        st.bu[u][c] = bf16_to_f32(S.b1[rowi * gpr + (ch >> 1)]);
-                    }
-                }
-            }
-        }
-    };
-
-    Stage<BITS, CPL> A, B;
-    if (iters > 0) load(A, 0);
-
-    // This lane's activations and their chunk sums.
-    float xr[CPL][32];
-    float xs[CPL];
-    const void *xb = S.x_bf16
-        ? (const void *)(static_cast<const uint16_t *>(S.x) + (size_t)slot * S.x_slot_stride)
-        : (const void *)(static_cast<const float *>(S.x) + (size_t)slot * S.x_slot_stride);
-#pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        const int ch = j + c * lpr;
-        xs[c] = 0.f;
-        if (ch < nchunk) {
-            load_x32(xr[c], xb, S.x_bf16, ch * 32);
-#pragma unroll
-            for (int i = 0; i < 32; i++) xs[c] += xr[c][i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; i++) xr[c][i] = 0.f;
-        }
-    }
-
-    auto consume = [&](const Stage<BITS, CPL> &st, int it) {
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int r = (wi + (it * kU + u) * W) * rpw + g;
-            float a = 0.f, b = 0.f;
-#pragma unroll
-            for (int c = 0; c < CPL; c++) {
-                const int ch = j + c * lpr;
-                if (ch < nchunk) {
-                    a += st.s[u][c] * chunk_dot<BITS>(st.w[u][c], xr[c]) + st.b[u][c] * xs[c];
-                    if (gated) b += st.su[u][c] * chunk_dot<BITS>(st.u[u][c], xr[c]) + st.bu[u][c] * xs[c];
-                }
-            }
-            a = group_sum(a, lpr);
-            if (gated) b = group_sum(b, lpr);
-            if (j == 0 && r < S.rows) {
-                const float v = bad_id ? __builtin_nanf("") : (gated ? siluf_(a) * b : a);
-                const size_t o = (size_t)slot * S.rows + r;
-                if (S.y_bf16)
-                    static_cast<uint16_t *>(S.y)[o] = f32_to_bf16(v);
-                else
-                    static_cast<float *>(S.y)[o] = v;
-            }
-        }
-    };
-
-    for (int it = 0; it < iters; it += 2) {
-        if (it + 1 < iters) load(B, it + 1);
-        consume(A, it);
-        if (it + 1 < iters) {
-            if (it + 2 < iters) load(A, it + 2);
-            consume(B, it + 1);
-        }
-    }
+    if (S.p1)
+        qmv_wave<BITS, CPL, true, D>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k]);
+    else
+        qmv_wave<BITS, CPL, false, D>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k]);
 }
 
 static int pow2ceil(int v) {
@@ -184,8 +194,8 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
     QmvParams P{};
     P.nseg = nseg;
     int cpl = 1;
-    long want = 0;
     long groups[kMaxSeg];
+    long total = 0;
     for (int i = 0; i < nseg; i++) {
         P.seg[i] = segs[i];
         if (segs[i].top8 && (!top8 || !top8->logits || segs[i].count != 8)) {
@@ -198,33 +208,43 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
         if (c > cpl) cpl = c;
         P.lpr[i] = lpr;
         groups[i] = (segs[i].rows + (64 / lpr) - 1) / (64 / lpr);
-        want += ((groups[i] + 4 * kU - 1) / (4 * kU)) * segs[i].count;
+        total += groups[i] * segs[i].count;
     }
-    // Blocks per slot: enough for one stage per wave, capped near kBlocksTarget overall
-    // (each wave then walks several stages with the next one in flight).
+    // Row groups per wave: one while the launch has at most kWavesTarget row groups,
+    // else enough that the waves number about kWavesTarget.
+    const long per = std::max(1L, (total + kWavesTarget - 1) / kWavesTarget);
+    int kmax = 1;
     int blocks = 0;
     for (int i = 0; i < nseg; i++) {
-        long full = (groups[i] + 4 * kU - 1) / (4 * kU);
-        long bps = full;
-        if (want > kBlocksTarget) bps = std::max(1L, (full * kBlocksTarget + want - 1) / want);
-        P.blocks_per_slot[i] = (int)bps;
+        const long w = (groups[i] + per - 1) / per;
+        const long it = (groups[i] + w - 1) / w;
+        P.waves_per_slot[i] = (int)w;
+        P.iters[i] = (int)it;
+        P.blocks_per_slot[i] = (int)((w + 3) / 4);
+        if (it > kmax) kmax = (int)it;
         P.start[i] = blocks;
-        blocks += (int)bps * segs[i].count;
+        blocks += P.blocks_per_slot[i] * segs[i].count;
     }
     P.start[nseg] = blocks;
     if (top8) P.top8 = *top8;
-    dim3 grid(blocks), block(256);
-#define DIH_QMV_CASE(B, C)                                                \
-    if (bits == B && cpl <= C) {                                          \
-        DIH_LAUNCH((qmv_kernel<B, C>), grid, block, 0, s, P);             \
-        return hip_ok(hipGetLastError(), error, capacity, "qmv launch");  \
+    // ring depth: up to four row groups in flight; wide rows (C > 2048) hold more
+    // registers per group, so their depth is capped to stay clear of spills
+    int depth = kmax >= 4 ? 4 : kmax >= 2 ? 2 : 1;
+    if (cpl == 2 && depth > 2) depth = 2;
+    if (cpl > 2) {
+        cpl = 4;
+        depth = 1;
     }
-    DIH_QMV_CASE(8, 1)
-    DIH_QMV_CASE(8, 2)
-    DIH_QMV_CASE(8, 4)
-    DIH_QMV_CASE(5, 1)
-    DIH_QMV_CASE(5, 2)
-    DIH_QMV_CASE(5, 4)
+    dim3 grid(blocks), block(256);
+#define DIH_QMV_CASE(B, C, D)                                                  \
+    if (bits == B && cpl <= C && depth == D) {                                  \
+        DIH_LAUNCH((qmv_kernel<B, C, D>), grid, block, 0, s, P);               \
+        return hip_ok(hipGetLastError(), error, capacity, "qmv launch");       \
+    }
+    DIH_QMV_CASE(8, 1, 1) DIH_QMV_CASE(8, 1, 2) DIH_QMV_CASE(8, 1, 4)
+    DIH_QMV_CASE(8, 2, 1) DIH_QMV_CASE(8, 2, 2) DIH_QMV_CASE(8, 4, 1)
+    DIH_QMV_CASE(5, 1, 1) DIH_QMV_CASE(5, 1, 2) DIH_QMV_CASE(5, 1, 4)
+    DIH_QMV_CASE(5, 2, 1) DIH_QMV_CASE(5, 2, 2) DIH_QMV_CASE(5, 4, 1)
 #undef DIH_QMV_CASE
     set_error(error, capacity, "Unsupported GEMV shape");
     return false;
@@ -255,29 +275,30 @@ __global__ __launch_bounds__(512) void moe_down_merge_kernel(
     const int row0 = blockIdx.x * ROWS;
     const uint32_t e = ids[slot];
     // weights first: every pass of this wave in flight at once
+    // raw words first (bf16 bit patterns converted only when consumed), every pass of this
+    // wave in flight at once; lanes past the row's chunks load a clamped chunk and are masked
+    const bool valid = j < nchunk;
+    const int jc = valid ? j : nchunk - 1;
     Chunk<BITS> wc[PASSES];
-    float sc[PASSES], bc[PASSES];
+    uint32_t sc[PASSES], bc[PASSES];
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
         int h = row0 + p * GROUPS + g;
         h = h < H ? h : H - 1;
         const size_t rowi = (size_t)e * H + h;
-        if (j < nchunk) {
-            load_chunk<BITS>(wc[p], packed + rowi * wpr, j);
-            sc[p] = bf16_to_f32(scales[rowi * gpr + (j >> 1)]);
-            bc[p] = bf16_to_f32(biases[rowi * gpr + (j >> 1)]);
-        }
+        load_chunk<BITS>(wc[p], packed + rowi * wpr, jc);
+        sc[p] = scales[rowi * gpr + (jc >> 1)];
+        bc[p] = biases[rowi * gpr + (jc >> 1)];
     }
     float xr[32];
     float xs = 0.f;
-    if (j < nchunk) {
-        load_x32(xr, act + (size_t)slot * I, 0, j * 32);
+    load_x32(xr, act + (size_t)slot * I, 0, jc * 32);
 #pragma unroll
-        for (int i = 0; i < 32; i++) xs += xr[i];
-    }
+    for (int i = 0; i < 32; i++) xs += xr[i];
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
-        float v = j < nchunk ? sc[p] * chunk_dot<BITS>(wc[p], xr) + bc[p] * xs : 0.f;
+        float v = bf16_to_f32(sc[p]) * chunk_dot<BITS>(wc[p], xr) + bf16_to_f32(bc[p]) * xs;
+        v = valid ? v : 0.f;
         v = group_sum(v, LPR);
         if (j == 0) part[slot][p * GROUPS + g] = v;
     }

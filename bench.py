@@ -7,12 +7,18 @@ sigmoid gate) as achieved HBM GB/s of its algorithmic bytes. The other configs a
 measured in the same run and reported under "secondary". Weights and activations are
 seeded synthetic data created on the GPU; every timed step reads weights that are not
 resident in the 256 MB Infinity Cache (rotating copies whose working set between reuses
-exceeds 512 MB). Timed loops are captured in HIP graphs and replayed; per-stage HIP events
-inside the graph (on the stream the kernels run on) give each kernel's average duration
-over the timed region.
+exceeds 512 MB). The timed loop (exactly --steps steps) is captured in a HIP graph and
+replayed between two synchronizations; `value` and `ms_per_step` come from that wall
+clock. Per-kernel durations come from HIP event pairs that the library records on the
+launch stream around every kernel (hipExtLaunchKernelGGL start/stop events) while the
+same steps run again directly after the timed replay; `roofline.achieved` is the dominant
+kernel's algorithmic bytes per launch over its average duration. `roofline.traffic` is
+the HBM bytes per launch that rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE measured for that
+kernel, scaled by the counters' reading for a plain copy of known size, read from the
+summaries committed under profiles/ (null when none is present).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|qmv|prefill|
-                 prefill5|dense|lm_head] [--cpu-seconds S] [--no-cpu]
+                 prefill5|dense|lm_head|copycal] [--layers L] [--cpu-seconds S] [--no-cpu]
 """
 import argparse
 import json
@@ -39,6 +45,20 @@ def metric_name():
 def qbytes(experts, rows, cols, bits):
     """Algorithmic bytes of a packed matrix: codes + bf16 scale + bf16 bias per 64."""
     return experts * rows * (cols * bits // 8 + (cols // 64) * 4)
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summaries
+    (a line `traffic_bytes_per_launch[<kernel>]: <bytes>` in profiles/*.md), else None."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_launch\[([^\]]+)\]:\s*([0-9.eE+]+)", line)
+                if m and m.group(1) == kernel:
+                    return float(m.group(2))
+    return None
 
 
 def log(msg):
@@ -143,10 +163,13 @@ class Bench:
         ms, prof = self.timed_graph(step, steps, warmup)
         w_bytes = 9 * (2 * qbytes(1, I, H, 8) + qbytes(1, H, I, 8)) + qbytes(1, E, H, 8) + qbytes(1, 1, H, 8)
         step_bytes = w_bytes + H * 2 + 2 * H * 2   # + x read, residual read/write
+        # algorithmic bytes of each of the three launches: weights + activations read and
+        # results written (router logits/candidates and ids/probs are a few hundred bytes)
         stage_bytes = {
-            "decode_router_shared": qbytes(1, E, H, 8) + qbytes(1, 1, H, 8) + 2 * qbytes(1, I, H, 8) + H * 2,
-            "decode_experts_gate_up": 16 * qbytes(1, I, H, 8) + qbytes(1, H, I, 8) + H * 2,
-            "decode_down_merge": 8 * qbytes(1, H, I, 8) + 2 * H * 2,
+            "decode_router_shared": qbytes(1, E, H, 8) + qbytes(1, 1, H, 8) + 2 * qbytes(1, I, H, 8) + H * 2
+                                    + E * 4 + I * 4,
+            "decode_experts_gate_up": 16 * qbytes(1, I, H, 8) + H * 2 + 8 * I * 4,
+            "decode_down_merge": 9 * qbytes(1, H, I, 8) + 9 * I * 4 + 2 * H * 2,
         }
         stages = {}
         for name, (tot, cnt) in prof.items():
@@ -286,6 +309,18 @@ class Bench:
                 "qmv_kernel_avg_us": kern * 1e3,
                 "qmv_kernel_GB_s": (b - 248320 * 4) / (kern * 1e-3) / 1e9 if kern > 0 else None}
 
+    def copycal(self, steps, mbytes=512):
+        """A plain device copy of known size: the reference point that scales rocprofv3's
+        FETCH_SIZE / WRITE_SIZE counters to bytes."""
+        torch = self.torch
+        n = mbytes << 20
+        a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(steps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        return {"bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": steps}
+
     def free(self, built):
         for mats, _ in built:
             for m in mats.values():
@@ -329,6 +364,8 @@ def main():
     ap.add_argument("--workload", default="all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--layers", type=int, default=24,
+                    help="decode: rotating layer copies (24 x 855 MB keeps every step's weights out of the 256 MB MALL)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -342,7 +379,7 @@ def main():
     wl = args.workload
     res = {}
     if wl in ("all", "decode"):
-        res["decode"] = b.decode(steps, warmup)
+        res["decode"] = b.decode(steps, warmup, layers=args.layers)
         log(f"[decode] {res['decode']['GB_s']:.0f} GB/s, {res['decode']['ms_per_step'] * 1e3:.2f} us/step")
     if wl in ("all", "qmv"):
         res["qmv"] = b.qmv(steps, warmup)
@@ -356,6 +393,9 @@ def main():
     if wl in ("all", "dense"):
         res["dense"] = b.dense(steps, warmup)
         log(f"[dense] {res['dense']['TFLOP_s']:.1f} TFLOP/s")
+    if wl == "copycal":
+        print(json.dumps(b.copycal(max(1, min(steps, 8)))), flush=True)
+        return
     if wl in ("all", "lm_head"):
         res["lm_head"] = b.lm_head(steps, warmup)
         log(f"[lm_head] {res['lm_head']['GB_s']:.0f} GB/s")
@@ -373,7 +413,8 @@ def main():
             dom = max(d["stages"].items(), key=lambda kv: kv[1]["avg_us"])
             roof = {"kernel": dom[0], "bound": "hbm", "achieved": dom[1]["GB_s"], "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": dom[1]["GB_s"] / PEAK_HBM_GBS if dom[1]["GB_s"] else None,
-                    "traffic": None, "avg_us": dom[1]["avg_us"], "bytes_per_launch": dom[1]["bytes"]}
+                    "traffic": traffic_from_profiles(dom[0]), "avg_us": dom[1]["avg_us"],
+                    "bytes_per_launch": dom[1]["bytes"]}
     else:
         k, v = next(iter(res.items()))
         head = {"metric": metric_name(), "value": v.get("GB_s") or v.get("TFLOP_s"),

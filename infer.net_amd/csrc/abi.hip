@@ -621,12 +621,6 @@ __attribute__((visibility("default"))) int dih_top8(void *ctx, const void *logit
                : -1;
 }
 
-static size_t max_chunks_for(int tokens, int experts, int with_shared) {
-    size_t routed = (size_t)tokens * 8;
-    return (routed + 63) / 64 + std::min<size_t>((size_t)experts, routed) +
-           (with_shared ? ((size_t)tokens + 63) / 64 : 0);
-}
-
 __attribute__((visibility("default"))) int dih_build_groups(void *ctx, const uint32_t *ids, int tokens,
                                                             int experts, uint32_t *counts, uint32_t *routes,
                                                             void *stream, char *error, int capacity) {
@@ -635,14 +629,7 @@ __attribute__((visibility("default"))) int dih_build_groups(void *ctx, const uin
         set_error(error, capacity, "Invalid grouping arguments");
         return -1;
     }
-    int4 *chunks = static_cast<int4 *>(scratch(c, S_CHUNKS, max_chunks_for(tokens, experts, 0) * 16, error, capacity));
-    uint32_t *nch = static_cast<uint32_t *>(scratch(c, S_NCHUNKS, 16, error, capacity));
-    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
-    if (!chunks || !nch || !tk) return -1;
-    return launch_build_groups(ids, tokens, experts, 0, counts, routes, chunks, nch, tk + 2, pick(c, stream), error,
-                               capacity)
-               ? 0
-               : -1;
+    return launch_build_groups(ids, tokens, experts, 0, counts, routes, pick(c, stream), error, capacity) ? 0 : -1;
 }
 
 __attribute__((visibility("default"))) int dih_dequant_bf16(void *ctx, void *matrix, int expert, uint16_t *out,
@@ -821,35 +808,31 @@ __attribute__((visibility("default"))) int dih_moe_prefill(void *ctx, const dih_
         return -1;
     }
     const size_t T = (size_t)tokens, routes_n = T * 9;
-    const size_t maxc = max_chunks_for(tokens, E, 1);
     uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, std::max<size_t>(T * 8 * 4, 256), error, capacity));
     float *probs = static_cast<float *>(scratch(c, S_PROBS, T * 8 * 4, error, capacity));
     uint32_t *counts = static_cast<uint32_t *>(scratch(c, S_COUNTS, (size_t)(E + 1) * 4, error, capacity));
     uint32_t *routes = static_cast<uint32_t *>(scratch(c, S_ROUTES, (size_t)(E + 1) * T * 4, error, capacity));
-    int4 *chunks = static_cast<int4 *>(scratch(c, S_CHUNKS, maxc * 16, error, capacity));
-    uint32_t *nch = static_cast<uint32_t *>(scratch(c, S_NCHUNKS, 16, error, capacity));
-    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
     uint16_t *actb = static_cast<uint16_t *>(scratch(c, S_ACTBF, routes_n * I * 2, error, capacity));
     float *rout = static_cast<float *>(scratch(c, S_ROUTEOUT, routes_n * H * 4, error, capacity));
-    if (!ids || !probs || !counts || !routes || !chunks || !nch || !tk || !actb || !rout) return -1;
+    if (!ids || !probs || !counts || !routes || !actb || !rout) return -1;
     float *route_out = trace && trace->expert_out ? trace->expert_out : rout;
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);
     if (!launch_top8(logits, logits_dtype == DIH_BF16, tokens, E, ids, probs, trace ? trace->status : nullptr,
-                     trace ? trace->logits : nullptr, tk + 3, s, error, capacity))
+                     trace ? trace->logits : nullptr, nullptr, s, error, capacity))
         return -1;
     prof_mark(c, s, "prefill_top8");
-    if (!launch_build_groups(ids, tokens, E, 1, counts, routes, chunks, nch, tk + 3, s, error, capacity)) return -1;
+    if (!launch_build_groups(ids, tokens, E, 1, counts, routes, s, error, capacity)) return -1;
     prof_mark(c, s, "prefill_group");
     QmmArgs a;
-    a.m0 = gate; a.m1 = up; a.sm0 = sg; a.sm1 = su; a.tokens = tokens; a.routes = routes; a.chunks = chunks;
-    a.nchunks = nch; a.max_chunks = (int)maxc; a.x = static_cast<const uint16_t *>(x); a.in_mode = 1;
+    a.m0 = gate; a.m1 = up; a.sm0 = sg; a.sm1 = su; a.tokens = tokens; a.routes = routes; a.counts = counts;
+    a.ngroups = E + 1; a.x = static_cast<const uint16_t *>(x); a.in_mode = 1;
     a.y = actb; a.y_bf16 = 1;
     if (!launch_qmm(a, s, error, capacity)) return -1;
     prof_mark(c, s, "prefill_gate_up");
     QmmArgs d;
-    d.m0 = down; d.sm0 = sd; d.tokens = tokens; d.routes = routes; d.chunks = chunks; d.nchunks = nch;
-    d.max_chunks = (int)maxc; d.x = actb; d.in_mode = 0; d.y = route_out; d.y_bf16 = 0;
+    d.m0 = down; d.sm0 = sd; d.tokens = tokens; d.routes = routes; d.counts = counts; d.ngroups = E + 1;
+    d.x = actb; d.in_mode = 0; d.y = route_out; d.y_bf16 = 0;
     if (!launch_qmm(d, s, error, capacity)) return -1;
     prof_mark(c, s, "prefill_down");
     if (!launch_moe_merge(sr, static_cast<const uint16_t *>(x), tokens, H, route_out, probs,

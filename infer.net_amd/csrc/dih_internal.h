@@ -130,20 +130,18 @@ bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, u
                  hipStream_t s, char *error, int capacity);
 
 bool launch_build_groups(const uint32_t *ids, int tokens, int experts, int with_shared,
-                         uint32_t *counts, uint32_t *routes, int4 *chunks, uint32_t *nchunks,
-                         uint32_t *ticket, hipStream_t s, char *error, int capacity);
+                         uint32_t *counts, uint32_t *routes, hipStream_t s, char *error, int capacity);
 
 struct QmmArgs {
     // routed matrices (gate or down) and optional up for the gated kernel
     const Matrix *m0 = nullptr, *m1 = nullptr;
-    // shared-expert matrices used for chunks whose expert == experts
+    // shared-expert matrices used for the group with index == experts
     const Matrix *sm0 = nullptr, *sm1 = nullptr;
     int tokens = 0;         // T
-    int dense = 0;          // 1: identity routes over `tokens`, no chunk list
-    const uint32_t *routes = nullptr;   // [(E+1)*T]
-    const int4 *chunks = nullptr;       // (expert, start, n, 0)
-    const uint32_t *nchunks = nullptr;  // device count
-    int max_chunks = 0;
+    int dense = 0;          // 1: identity routes over `tokens`, no groups
+    const uint32_t *routes = nullptr;   // [ngroups * T] ascending route lists
+    const uint32_t *counts = nullptr;   // [ngroups] device
+    int ngroups = 0;                    // experts (+1 with a shared expert)
     const uint16_t *x = nullptr;        // bf16 input rows
     int in_mode = 0;                    // 0: row = route; 1: gate input row (route/8, shared)
     void *y = nullptr; int y_bf16 = 0;  // output rows indexed by route

@@ -77,17 +77,13 @@ bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, u
 // Block e lists the routes r (= token*8 + slot) with ids[r] == e in ascending order
 // (prefill_build_groups prefill_moe.mm:8-17 uses a SIMD prefix sum per 32 routes; here a
 // 256-thread ballot/prefix pass per 256 routes). Block `experts` (when with_shared) lists
-// the shared expert's routes T*8 + t for every token. The last block to finish builds the
-// chunk list in expert order: ceil(count/64) chunks per expert, (expert, start, n), which
-// makes the order deterministic where the reference's atomic tile append is not
-// (prefill_moe.mm:15).
+// the shared expert's routes T*8 + t for every token. Blocks do not communicate: the GEMM
+// derives its chunks from the counts (in expert order, so the order is deterministic where
+// the reference's atomic tile append, prefill_moe.mm:15, is not).
 __global__ __launch_bounds__(256) void group_kernel(const uint32_t *ids, int tokens, int experts,
                                                     int with_shared, uint32_t *counts,
-                                                    uint32_t *routes, int4 *chunks,
-                                                    uint32_t *nchunks, uint32_t *ticket) {
+                                                    uint32_t *routes) {
     __shared__ uint32_t wave_tot[4];
-    __shared__ int last;
-    __shared__ uint32_t scan[257];
     const int e = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T8 = tokens * 8;
@@ -95,59 +91,31 @@ __global__ __launch_bounds__(256) void group_kernel(const uint32_t *ids, int tok
     if (e == experts) {
         for (int t = tid; t < tokens; t += 256) out[t] = (uint32_t)(T8 + t);
         if (tid == 0) counts[e] = (uint32_t)tokens;
-    } else {
-        uint32_t total = 0;
-        for (int base = 0; base < T8; base += 256) {
-            const int r = base + tid;
-            const bool sel = r < T8 && ids[r] == (uint32_t)e;
-            const unsigned long long mask = __ballot(sel);
-            const uint32_t below = (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
-            if (lane == 0) wave_tot[wave] = (uint32_t)__popcll(mask);
-            __syncthreads();
-            uint32_t off = total;
-            for (int w = 0; w < wave; w++) off += wave_tot[w];
-            // A token lists an expert at most once, so count <= tokens; ids that repeat an
-            // expert within a token are truncated here instead of overrunning the list.
-            if (sel && off + below < (uint32_t)tokens) out[off + below] = (uint32_t)r;
-            total += wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
-            __syncthreads();
-        }
-        if (tid == 0) counts[e] = min(total, (uint32_t)tokens);
+        return;
     }
-    // last block: chunk list
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = (atomicAdd(ticket, 1u) == gridDim.x - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const int n = experts + with_shared;  // <= 257
-    for (int i = tid; i < n; i += 256) scan[i] = (counts[i] + 63u) / 64u;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t acc = 0;
-        for (int i = 0; i < n; i++) {
-            uint32_t v = scan[i];
-            scan[i] = acc;
-            acc += v;
-        }
-        *nchunks = acc;
-        *ticket = 0u;
+    uint32_t total = 0;
+    for (int base = 0; base < T8; base += 256) {
+        const int r = base + tid;
+        const bool sel = r < T8 && ids[r] == (uint32_t)e;
+        const unsigned long long mask = __ballot(sel);
+        const uint32_t below = (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_tot[wave] = (uint32_t)__popcll(mask);
+        __syncthreads();
+        uint32_t off = total;
+        for (int w = 0; w < wave; w++) off += wave_tot[w];
+        // A token lists an expert at most once, so count <= tokens; ids that repeat an
+        // expert within a token are truncated here instead of overrunning the list.
+        if (sel && off + below < (uint32_t)tokens) out[off + below] = (uint32_t)r;
+        total += wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+        __syncthreads();
     }
-    __syncthreads();
-    for (int i = tid; i < n; i += 256) {
-        const uint32_t c = counts[i];
-        uint32_t at = scan[i];
-        for (uint32_t s = 0; s < c; s += 64, at++)
-            chunks[at] = make_int4(i, (int)s, (int)min(64u, c - s), 0);
-    }
+    if (tid == 0) counts[e] = min(total, (uint32_t)tokens);
 }
 
 bool launch_build_groups(const uint32_t *ids, int tokens, int experts, int with_shared,
-                         uint32_t *counts, uint32_t *routes, int4 *chunks, uint32_t *nchunks,
-                         uint32_t *ticket, hipStream_t s, char *error, int capacity) {
-    DIH_LAUNCH(group_kernel, dim3(experts + with_shared), dim3(256), 0, s, ids, tokens,
-                       experts, with_shared, counts, routes, chunks, nchunks, ticket);
+                         uint32_t *counts, uint32_t *routes, hipStream_t s, char *error, int capacity) {
+    DIH_LAUNCH(group_kernel, dim3(experts + with_shared), dim3(256), 0, s, ids, tokens, experts,
+               with_shared, counts, routes);
     return hip_ok(hipGetLastError(), error, capacity, "grouping launch");
 }
 

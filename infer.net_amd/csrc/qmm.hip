@@ -1,74 +1,185 @@
 // Grouped (MoE) and dense quantized GEMM on gfx950 bf16 MFMA.
 //
-// Each block owns 128 weight rows (four waves x 32 rows) of one expert and one chunk
-// of up to 32*NT routes of that expert. Every wave computes a 32-row x 32*NT-route tile
-// with v_mfma_f32_32x32x16_bf16 and fp32 accumulators over K in 64-column affine
-// groups.
+// Block: four waves sharing one tile of up to BN = 32*NT routes (tokens) of one expert; wave
+// w owns 32 weight rows (and, for the gated kernel, the same 32 rows of the up matrix),
+// so a block covers 128 weight rows. Each wave computes 32 rows x 32*ntiles routes with
+// v_mfma_f32_32x32x16_bf16 and fp32 accumulators, K streamed in 64-column affine groups.
 //
-// K permutation (no LDS needed for the weights): MFMA j (j = 0..3) of a 64-column group
-// takes its 16 K-slots from columns {32h + 8j + i : h in {0,1}, i in 0..7}, where h is
-// the lane's half of the wave. Then lane (row r, half h) needs exactly the 32
-// consecutive codes [32h, 32h+32) of its row in that group (one Chunk: 32 bytes 8-bit,
-// 20 bytes 5-bit) and lane (route n, half h) needs the 32 consecutive bf16 activations
-// [32h, 32h+32) of its route. Both are dequantized/loaded straight into MFMA operand
-// registers. Dequantized weights are bf16(fp32(q*scale+bias)) with round-to-nearest-even
-// and activations are bf16, so operand values match the reference's BF16 path
-// (prefill_expert_packed.mm:24-35, 64-65); accumulation order differs (fp32).
+// K permutation: MFMA j (j = 0..3) of a 64-column group takes its 16 K-slots from columns
+// {32h + 8j + i : h in {0,1}, i in 0..7}, h being the lane's half of the wave. Lane
+// (row r, half h) then needs exactly the 32 consecutive codes [32h, 32h+32) of its row in
+// that group (one Chunk: 32 bytes 8-bit, 20 bytes 5-bit), dequantized in registers
+// straight into MFMA A operands as bf16(fp32(q*scale+bias)) with round-to-nearest-even
+// (the rounding of prefill_expert_packed.mm:24-35), and lane (route n, half h) needs the
+// 32 consecutive bf16 activations [32h, 32h+32) of its route.
 //
-// Work order: the route chunks are listed expert by expert (ascending), chunks of one
-// expert consecutive. Logical block L = rowtile * n_chunks + chunk, and physical block b
-// runs logical (b % 8) * ceil(n_work / 8) + b / 8, so consecutive logical blocks land on
-// the same XCD at nearly the same time: chunks of one popular expert then share that
-// expert's weight rows in the XCD's L2. Blocks past n_work exit at once, which replaces
-// the reference's indirect dispatch (prefill_group_dispatch, prefill_moe.mm:18-22).
+// Activations (B): the block gathers each K step's tile (routes x 64 bf16) from global
+// memory by route (gate/up: token row = route/8, shared expert rows after the routed ones;
+// down: row = route) into an LDS double buffer whose rows are padded to 144 bytes, so the
+// 16-byte MFMA operand reads of 32 consecutive routes hit distinct banks. The next step's
+// tile is fetched into registers while the current step's MFMAs run.
+//
+// Pipeline: a K step's weight words (codes and the raw bf16 bits of scales and biases) and
+// its activation tile are requested D steps before they are used, into register rings of
+// depth D. Vector-memory counters retire in issue order, so the only waits are for loads
+// issued D-1 steps earlier: the weight words of the current step, and the activation tile
+// of the next step, which is written to the other LDS buffer after this step's MFMAs.
+//
+// Work: grouped launches list no chunks on the host. Every block reads the E(+1) route
+// counts, forms ceil(count/BN) chunks per expert in expert order with a wave prefix sum and
+// finds its own (row tile, chunk); blocks past the work exit. Logical work item
+// L = rowtile * n_chunks + chunk runs on physical block b with L = (b % 8) * ceil(W/8) +
+// b / 8, so consecutive items land on one XCD at nearly the same time and chunks of one
+// popular expert share that expert's weight rows in the XCD's L2. This replaces the
+// reference's atomic tile list and indirect dispatch (prefill_moe.mm:8-22) with a
+// deterministic order.
 #include "dih_device.h"
 #include "dih_internal.h"
 
 namespace dih {
 
+namespace {
+
+constexpr int kRowPad = 72;          // bf16 per LDS activation row (64 + 8 pad = 144 B)
+
 struct QmmParams {
     const uint32_t *p0, *p1; const uint16_t *s0, *s1, *b0, *b1;     // routed
     const uint32_t *sp0, *sp1; const uint16_t *ss0, *ss1, *sb0, *sb1;  // shared expert
     int experts, rows, columns, tokens, dense, in_mode, y_bf16, row_tiles;
-    const uint32_t *routes; const int4 *chunks; const uint32_t *nchunks;
+    int ngroups;                       // experts (+1 with a shared expert)
+    const uint32_t *routes;            // [ngroups * tokens]
+    const uint32_t *counts;            // [ngroups]
+    int max_work;                      // grid work items (upper bound)
     const uint16_t *x; void *y;
 };
 
-template <int BITS>
+template <int BITS, bool GATED>
 struct KStep {
-    Chunk<BITS> a0, a1;
-    float s0, bb0, s1, bb1;
+    Chunk<BITS> a0;
+    Chunk<BITS> a1[1];
+    uint32_t s0, bb0, s1, bb1;
 };
 
-template <int BITS, bool GATED, int NT>
-__global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
-    const int n_chunks = P.dense ? (P.tokens + 63) / 64 : (int)*P.nchunks;
-    const int n_work = P.row_tiles * n_chunks;
-    const int per = (n_work + 7) / 8;
-    const int b = blockIdx.x;
-    const int jj = b >> 3;
-    if (jj >= per) return;
-    const int L = (b & 7) * per + jj;
-    if (L >= n_work) return;
-    const int rt = L / n_chunks, ci = L - rt * n_chunks;
-
-    int e, start, nvalid;
-    if (P.dense) {
-        e = 0; start = ci * 64; nvalid = min(64, P.tokens - start);
-    } else {
-        int4 c = P.chunks[ci];
-        e = c.x; start = c.y; nvalid = c.z;
+// Chunks of up to BN routes per group, in group order: returns the group of chunk `ci`
+// and the chunk's first route within that group, plus the total number of chunks. One
+// wave; every lane receives the result.
+template <int BN>
+DIH_DEV int chunk_of(const uint32_t *counts, int ngroups, int ci, int &group, int &first, int &count) {
+    const int lane = threadIdx.x & 63;
+    // lane l owns groups 5l .. 5l+4 (ngroups <= 320)
+    int cnt[5], raw[5], run = 0;
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+        const int g = lane * 5 + i;
+        raw[i] = g < ngroups ? (int)counts[g] : 0;
+        cnt[i] = (raw[i] + BN - 1) / BN;
+        run += cnt[i];
     }
+    // inclusive wave prefix sum of the lane totals
+    int incl = run;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, 63, 64);
+    const int excl = incl - run;
+    // the lane whose range holds chunk ci
+    const bool mine = ci >= excl && ci < incl;
+    const unsigned long long m = __ballot(mine);
+    const int owner = m ? (int)__builtin_ctzll(m) : 0;
+    int g = 0, f = 0, n = 0;
+    if (mine) {
+        int c = ci - excl;
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            if (c >= 0 && c < cnt[i]) { g = lane * 5 + i; f = c * BN; n = raw[i]; }
+            c -= cnt[i];
+        }
+    }
+    group = __shfl(g, owner, 64);
+    first = __shfl(f, owner, 64);
+    count = __shfl(n, owner, 64);
+    return total;
+}
+
+// The MFMAs of one 64-column K step over the first NTU route tiles; each 16-column slice's
+// B operands are read from LDS before its MFMAs so the reads overlap.
+template <bool GATED, int NTU, int NT>
+DIH_DEV void mfma_step(const uint16_t *bb, const dih_bf16x8 (&a0)[4], const dih_bf16x8 (&a1)[4],
+                       dih_f32x16 (&acc0)[NT], dih_f32x16 (&acc1)[GATED ? NT : 1]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        dih_bf16x8 bx[NTU];
+#pragma unroll
+        for (int i = 0; i < NTU; i++)
+            bx[i] = *reinterpret_cast<const dih_bf16x8 *>(bb + (32 * i) * kRowPad + 8 * j);
+#pragma unroll
+        for (int i = 0; i < NTU; i++) {
+            acc0[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[j], bx[i], acc0[i], 0, 0, 0);
+            if constexpr (GATED)
+                acc1[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[j], bx[i], acc1[i], 0, 0, 0);
+        }
+    }
+}
+
+}  // namespace
+
+template <int BITS, bool GATED, int NT, int D>
+__global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
+    constexpr int BN = 32 * NT;
+    __shared__ __align__(16) uint16_t bs[2][BN * kRowPad];
+    __shared__ int xoff[BN];           // element offset of each route's input row
+    __shared__ int route_s[BN];
+    __shared__ int work[4];            // expert, first route, valid routes, row tile
+
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    // ---- which work item is this block? Physical block b runs logical item
+    // L = (b % 8) * (grid / 8) + b / 8 (consecutive items on one XCD at nearly the same time),
+    // item L = chunk * row_tiles + row tile.
+    if (wave == 0) {
+        int e = 0, first = 0, nvalid = 0, rt = -1;
+        const int b = blockIdx.x, per = (int)(gridDim.x >> 3);
+        const int L = (b & 7) * per + (b >> 3);
+        const int ci = L / P.row_tiles;
+        if (P.dense) {
+            if (ci * BN < P.tokens) {
+                rt = L - ci * P.row_tiles;
+                first = ci * BN;
+                nvalid = min(BN, P.tokens - first);
+            }
+        } else {
+            int count;
+            const int total = chunk_of<BN>(P.counts, P.ngroups, ci, e, first, count);
+            if (ci < total) {
+                rt = L - ci * P.row_tiles;
+                nvalid = min(BN, count - first);
+            }
+        }
+        if (lane == 0) { work[0] = e; work[1] = first; work[2] = nvalid; work[3] = rt; }
+    }
+    __syncthreads();
+    const int rt = work[3];
+    if (rt < 0) return;
+    const int e = work[0], first = work[1], nvalid = work[2];
+    const int ntiles = (nvalid + 31) >> 5;
+    const int C = P.columns, R = P.rows, G = C >> 6;
+
+    // ---- the chunk's route ids first (their wait must not include the weight stream)
+    int my_route = 0;
+    if (t < BN) {
+        const int n = t < nvalid ? t : 0;
+        my_route = P.dense ? first + n : (int)P.routes[(size_t)e * P.tokens + first + n];
+    }
+
+    // ---- weights of this wave's 32 rows
     const bool shared = !P.dense && e == P.experts;
     const uint32_t *pw0 = shared ? P.sp0 : P.p0;
     const uint16_t *ps0 = shared ? P.ss0 : P.s0, *pb0 = shared ? P.sb0 : P.b0;
     const uint32_t *pw1 = shared ? P.sp1 : P.p1;
     const uint16_t *ps1 = shared ? P.ss1 : P.s1, *pb1 = shared ? P.sb1 : P.b1;
     const int eix = shared ? 0 : e;
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 31, h = lane >> 5;
-    const int R = P.rows, C = P.columns, G = C >> 6;
     const int row = rt * 128 + wave * 32 + r;
     const int rr = row < R ? row : R - 1;
     const size_t rowi = (size_t)eix * R + rr;
@@ -78,97 +189,112 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
     const uint16_t *sc0 = ps0 + rowi * G, *bi0 = pb0 + rowi * G;
     const uint16_t *sc1 = GATED ? ps1 + rowi * G : nullptr, *bi1 = GATED ? pb1 + rowi * G : nullptr;
 
-    // Route of each of this lane's columns (one per tile) and its input row.
-    const int T8 = P.tokens * 8;
-    const uint32_t *rlist = P.dense ? nullptr : P.routes + (size_t)e * P.tokens + start;
-    const uint16_t *xrow[NT];
-    int ntiles = (nvalid + 31) >> 5;
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        int n = t * 32 + r;
-        int nn = n < nvalid ? n : 0;
-        int route = P.dense ? start + nn : (int)rlist[nn];
-        int in_row = route;
-        if (P.in_mode == 1) in_row = route < T8 ? (route >> 3) : route - T8;
-        xrow[t] = P.x + (size_t)in_row * C + 32 * h;
-    }
-
-    dih_f32x16 acc0[NT], acc1[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) { acc0[t][i] = 0.f; acc1[t][i] = 0.f; }
-    }
-
-    KStep<BITS> cur, nxt;
-    auto load_step = [&](KStep<BITS> &k, int kg) {
+    KStep<BITS, GATED> ring[D];
+    auto load_a = [&](KStep<BITS, GATED> &k, int kg) {
+        kg = kg < G ? kg : G - 1;
         load_chunk<BITS>(k.a0, w0, 2 * kg + h);
-        k.s0 = bf16_to_f32(sc0[kg]);
-        k.bb0 = bf16_to_f32(bi0[kg]);
+        k.s0 = sc0[kg];
+        k.bb0 = bi0[kg];
         if constexpr (GATED) {
-            load_chunk<BITS>(k.a1, w1, 2 * kg + h);
-            k.s1 = bf16_to_f32(sc1[kg]);
-            k.bb1 = bf16_to_f32(bi1[kg]);
-        }
-    };
-    uint4 xb[NT][4], xn[NT][4];
-    auto load_x = [&](uint4 (&dst)[NT][4], int kg) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (t < ntiles) {
-                const uint4 *p = reinterpret_cast<const uint4 *>(xrow[t] + 64 * kg);
-#pragma unroll
-                for (int q = 0; q < 4; q++) dst[t][q] = p[q];
-            }
+            load_chunk<BITS>(k.a1[0], w1, 2 * kg + h);
+            k.s1 = sc1[kg];
+            k.bb1 = bi1[kg];
         }
     };
 
-    load_step(cur, 0);
-    load_x(xb, 0);
-    for (int kg = 0; kg < G; kg++) {
-        if (kg + 1 < G) {
-            load_step(nxt, kg + 1);
-            load_x(xn, kg + 1);
-        }
-        dih_bf16x8 a0[4], a1[4];
-        chunk_to_bf16<BITS>(cur.a0, cur.s0, cur.bb0, a0);
-        if constexpr (GATED) chunk_to_bf16<BITS>(cur.a1, cur.s1, cur.bb1, a1);
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (t < ntiles) {
+    for (int d = 0; d < D; d++) load_a(ring[d], d);
+
+    // ---- input rows of the chunk's routes (past nvalid: the first route's row)
+    const int T8 = P.tokens * 8;
+    if (t < BN) {
+        int in_row = my_route;
+        if (P.in_mode == 1) in_row = my_route < T8 ? (my_route >> 3) : my_route - T8;
+        route_s[t] = my_route;
+        xoff[t] = in_row * C;
+    }
+
+    __syncthreads();  // xoff ready
+    // ---- activation tile loader: thread t moves 16-byte piece p of routes n0 + 32*i
+    const int p = t & 7, n0 = t >> 3;
+    int xo[NT];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    dih_bf16x8 bx = __builtin_bit_cast(dih_bf16x8, xb[t][j]);
-                    acc0[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[j], bx, acc0[t], 0, 0, 0);
-                    if constexpr (GATED)
-                        acc1[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[j], bx, acc1[t], 0, 0, 0);
-                }
-            }
-        }
-        if (kg + 1 < G) {
-            cur = nxt;
+    for (int i = 0; i < NT; i++) xo[i] = xoff[i * 32 < nvalid ? n0 + 32 * i : n0] + 8 * p;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 bv[D][NT];
+    // (unconditional: tiles past ntiles re-read the first route's row, a cache hit, and
+    // keep the ring in registers)
+    auto load_b = [&](u32x4 (&v)[NT], int kg) {
+        kg = kg < G ? kg : G - 1;
 #pragma unroll
-            for (int t = 0; t < NT; t++)
+        for (int i = 0; i < NT; i++) v[i] = *reinterpret_cast<const u32x4 *>(P.x + xo[i] + 64 * kg);
+    };
+    auto store_b = [&](const u32x4 (&v)[NT], int buf) {
 #pragma unroll
-                for (int q = 0; q < 4; q++) xb[t][q] = xn[t][q];
+        for (int i = 0; i < NT; i++) *reinterpret_cast<u32x4 *>(&bs[buf][(n0 + 32 * i) * kRowPad + 8 * p]) = v[i];
+    };
+#pragma unroll
+    for (int d = 0; d < D; d++) load_b(bv[d], d);
+    store_b(bv[0], 0);
+    __syncthreads();
+
+    dih_f32x16 acc0[NT], acc1[GATED ? NT : 1];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc0[i][k] = 0.f;
+    }
+    if constexpr (GATED) {
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc1[i][k] = 0.f;
         }
     }
 
-    // Epilogue: lane holds column n = t*32 + r, rows 8*(i/4) + 4h + (i%4) of the tile.
+    for (int kg0 = 0; kg0 < G; kg0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int kg = kg0 + d;
+            if (kg < G) {
+                // keep each step's work inside its step: hoisting a later step's dequant
+                // would make this step wait for that step's loads
+                __builtin_amdgcn_sched_barrier(0);
+                const int buf = kg & 1;
+                dih_bf16x8 a0[4], a1[4];
+                chunk_to_bf16<BITS>(ring[d].a0, bf16_to_f32(ring[d].s0), bf16_to_f32(ring[d].bb0), a0);
+                if constexpr (GATED) chunk_to_bf16<BITS>(ring[d].a1[0], bf16_to_f32(ring[d].s1), bf16_to_f32(ring[d].bb1), a1);
+                // step kg + D: weights and activations (clamped in bounds past the end)
+                load_a(ring[d], kg + D);
+                load_b(bv[d], kg + D);
+                const uint16_t *bb = &bs[buf][r * kRowPad + 32 * h];
+                // all NT tiles, branch-free (tiles past ntiles compute on a repeated route and
+                // are not stored; for chunks of a few routes the weight stream, not the MFMA
+                // pipe, bounds the step)
+                mfma_step<GATED, NT, NT>(bb, a0, a1, acc0, acc1);
+                // the next step's activations (requested D-1 steps ago) into the other buffer
+                if (kg + 1 < G) store_b(bv[(d + 1) % D], buf ^ 1);
+                __syncthreads();
+            }
+        }
+    }
+
+    // ---- epilogue: lane holds route n = 32i + r, rows 8*(k/4) + 4h + (k%4) of the tile
     const int row_base = rt * 128 + wave * 32;
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int n = t * 32 + r;
-        if (t >= ntiles || n >= nvalid) continue;
-        const int route = P.dense ? start + n : (int)rlist[n];
+    for (int i = 0; i < NT; i++) {
+        const int n = 32 * i + r;
+        if (i >= ntiles || n >= nvalid) continue;
+        const int route = route_s[n];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int m0 = row_base + 8 * q + 4 * h;
             float v[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                float g = acc0[t][4 * q + k];
-                v[k] = GATED ? siluf_(g) * acc1[t][4 * q + k] : g;
+                const float g = acc0[i][4 * q + k];
+                if constexpr (GATED) v[k] = siluf_(g) * acc1[i][4 * q + k];
+                else v[k] = g;
             }
             const size_t o = (size_t)route * R + m0;
             // vector stores only where the row offset keeps them naturally aligned
@@ -177,8 +303,7 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
                     uint2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(P.y) + o) = pk;
                 } else {
-                    *reinterpret_cast<float4 *>(static_cast<float *>(P.y) + o) =
-                        make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4 *>(static_cast<float *>(P.y) + o) = make_float4(v[0], v[1], v[2], v[3]);
                 }
             } else {
 #pragma unroll
@@ -195,6 +320,15 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
     }
 }
 
+// Upper bound of (row tile, chunk) work items: sum_g ceil(count_g / BN) <= routes / BN +
+// (groups holding any route); a shared-expert group adds `tokens` routes.
+static size_t qmm_max_work(int rows, int tokens, int ngroups, int dense, int bn) {
+    const size_t row_tiles = (size_t)(rows + 127) / 128;
+    if (dense) return row_tiles * ((size_t)(tokens + bn - 1) / bn);
+    const size_t routes = (size_t)tokens * 9;
+    return row_tiles * (routes / bn + std::min<size_t>((size_t)ngroups, routes));
+}
+
 bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     QmmParams P{};
     const Matrix *m0 = a.m0, *m1 = a.m1;
@@ -205,25 +339,41 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     P.experts = m0->experts; P.rows = m0->rows; P.columns = m0->columns;
     P.tokens = a.tokens; P.dense = a.dense; P.in_mode = a.in_mode; P.y_bf16 = a.y_bf16;
     P.row_tiles = (m0->rows + 127) / 128;
-    P.routes = a.routes; P.chunks = a.chunks; P.nchunks = a.nchunks;
+    P.ngroups = a.ngroups;
+    P.routes = a.routes; P.counts = a.counts;
     P.x = a.x; P.y = a.y;
-    const int max_chunks = a.dense ? (a.tokens + 63) / 64 : a.max_chunks;
-    const long work = (long)P.row_tiles * max_chunks;
-    const long blocks = 8 * ((work + 7) / 8);
-    if (blocks <= 0 || blocks > 0x7fffffffL) {
+    if (!a.dense && (a.ngroups < 1 || a.ngroups > 320 || !a.routes || !a.counts)) {
+        set_error(error, capacity, "Invalid grouped qmm arguments");
+        return false;
+    }
+    // input row offsets (row * columns) are 32-bit in the kernel
+    if ((size_t)a.tokens * 9 * (size_t)m0->columns > 0x7fffffffu) {
+        set_error(error, capacity, "Chunk too large for one grouped/dense qmm launch");
+        return false;
+    }
+    // Route tile width: 64 routes for the gated kernel, 128 otherwise (measured faster on
+    // every config than narrower tiles with deeper rings: occupancy hides more latency).
+    const bool gated = m1 != nullptr;
+    const int nt = gated ? 2 : 4;
+    const int bn = 32 * nt;
+    const size_t work = qmm_max_work(m0->rows, a.tokens, a.ngroups, a.dense, bn);
+    const size_t blocks = 8 * ((work + 7) / 8);
+    if (blocks == 0 || blocks > 0x7fffffffu) {
         set_error(error, capacity, "Invalid qmm grid");
         return false;
     }
+    P.max_work = (int)work;
     dim3 grid((unsigned)blocks), block(256);
-    const bool gated = m1 != nullptr;
-    if (m0->bits == 8) {
-        if (gated) DIH_LAUNCH((qmm_kernel<8, true, 2>), grid, block, 0, s, P);
-        else DIH_LAUNCH((qmm_kernel<8, false, 2>), grid, block, 0, s, P);
-    } else {
-        if (gated) DIH_LAUNCH((qmm_kernel<5, true, 2>), grid, block, 0, s, P);
-        else DIH_LAUNCH((qmm_kernel<5, false, 2>), grid, block, 0, s, P);
+#define DIH_QMM_CASE(B, GT, N, D)                                                   \
+    if (m0->bits == B && gated == GT && nt == N) {                                  \
+        DIH_LAUNCH((qmm_kernel<B, GT, N, D>), grid, block, 0, s, P);                \
+        return hip_ok(hipGetLastError(), error, capacity, "qmm launch");            \
     }
-    return hip_ok(hipGetLastError(), error, capacity, "qmm launch");
+    DIH_QMM_CASE(8, true, 2, 2) DIH_QMM_CASE(8, false, 4, 2)
+    DIH_QMM_CASE(5, true, 2, 2) DIH_QMM_CASE(5, false, 4, 2)
+#undef DIH_QMM_CASE
+    set_error(error, capacity, "Unsupported qmm configuration");
+    return false;
 }
 
 }  // namespace dih

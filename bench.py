@@ -376,27 +376,28 @@ def main():
         sys.exit(2)
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     b = Bench(args)
-    wl = args.workload
+    wls = set(args.workload.split(","))
+    on = lambda name: "all" in wls or name in wls  # noqa: E731
     res = {}
-    if wl in ("all", "decode"):
+    if on("decode"):
         res["decode"] = b.decode(steps, warmup, layers=args.layers)
         log(f"[decode] {res['decode']['GB_s']:.0f} GB/s, {res['decode']['ms_per_step'] * 1e3:.2f} us/step")
-    if wl in ("all", "qmv"):
+    if on("qmv"):
         res["qmv"] = b.qmv(steps, warmup)
         log(f"[qmv] {res['qmv']['GB_s']:.0f} GB/s")
-    if wl in ("all", "prefill"):
+    if on("prefill"):
         res["prefill"] = b.prefill(max(2, steps // 12), min(warmup, 3))
         log(f"[prefill] {res['prefill']['TFLOP_s']:.1f} TFLOP/s, {res['prefill']['GB_s']:.0f} GB/s")
-    if wl in ("all", "prefill5"):
+    if on("prefill5"):
         res["prefill5"] = b.prefill(max(2, steps // 24), min(warmup, 2), T=2048, bits=5, routing="uniform")
         log(f"[prefill5] {res['prefill5']['TFLOP_s']:.1f} TFLOP/s, {res['prefill5']['GB_s']:.0f} GB/s")
-    if wl in ("all", "dense"):
+    if on("dense"):
         res["dense"] = b.dense(steps, warmup)
         log(f"[dense] {res['dense']['TFLOP_s']:.1f} TFLOP/s")
-    if wl == "copycal":
+    if "copycal" in wls:
         print(json.dumps(b.copycal(max(1, min(steps, 8)))), flush=True)
         return
-    if wl in ("all", "lm_head"):
+    if on("lm_head"):
         res["lm_head"] = b.lm_head(steps, warmup)
         log(f"[lm_head] {res['lm_head']['GB_s']:.0f} GB/s")
 
@@ -427,7 +428,7 @@ def main():
         tok = {"decode_path_tok_s": 1e3 / per_token_ms,
                "note": "kernel-sum of this path only (40 MoE layers + lm_head), not model throughput"}
     cpu = None
-    if not args.no_cpu and wl in ("all", "decode"):
+    if not args.no_cpu and on("decode"):
         log(f"[cpu] timing the CPU baseline for ~{args.cpu_seconds:.0f} s")
         cpu = cpu_baseline(args.cpu_seconds)
     line = {"metric": head["metric"], "value": head["value"], "unit": head["unit"], "n_gpus": 1,

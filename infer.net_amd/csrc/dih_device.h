@@ -20,11 +20,13 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float dih_f32x4;
 
 DIH_DEV float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// Round-to-nearest-even f32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+// Round-to-nearest-even f32 -> bf16, two values per v_cvt_pk_bf16_f32 (gfx950). Written
+// as one instruction: from the vector-of-two form the compiler emits one conversion per
+// value plus a v_perm_b32 to merge them.
 DIH_DEV uint32_t pack_bf16x2(float lo, float hi) {
-    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-    bf16x2 v = {(__bf16)lo, (__bf16)hi};
-    return __builtin_bit_cast(uint32_t, v);
+    uint32_t r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
 }
 DIH_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 

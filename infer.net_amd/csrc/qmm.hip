@@ -46,6 +46,7 @@ struct QmmParams {
     const uint32_t *p0, *p1; const uint16_t *s0, *s1, *b0, *b1;     // routed
     const uint32_t *sp0, *sp1; const uint16_t *ss0, *ss1, *sb0, *sb1;  // shared expert
     int experts, rows, columns, tokens, dense, in_mode, y_bf16, row_tiles;
+    int rtb, rt_groups;                // streaming kernel: row tiles per block, groups of them
     int ngroups;                       // experts (+1 with a shared expert)
     const uint32_t *routes;            // [ngroups * tokens]
     const uint32_t *counts;            // [ngroups]
@@ -320,6 +321,307 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Streaming variant for K a multiple of 512 (every model shape): weight codes and activation
+// tiles reach LDS through direct global->LDS loads (global_load_lds), S stages deep, so the
+// memory instructions are coalesced (a weight tile is read four lanes per 64-byte row
+// segment; an activation tile eight lanes per 128-byte route segment) instead of one
+// lane per row. Both tiles are stored with a 16-byte-piece swizzle that makes the MFMA
+// operand reads conflict-free:
+//   weights, 8-bit : row r, piece p (of 4) at r*64 + 16*(p ^ ((r >> 2) & 3))
+//   weights, 5-bit : row r, dword d (of 10) at (r*10 + d)*4 (10 is coprime to 32 banks/2)
+//   activations    : route n, piece p (of 8) at n*128 + 16*(p ^ ((n >> 1) & 7))
+// Scales and biases come from registers: each lane loads its row's bf16 bits for eight
+// groups at a time (one 16-byte load per array per eight K steps).
+// One explicit vmcnt wait and one barrier per K step: step kg's copies were issued S-1
+// steps earlier; the copies of the following S-2 steps stay in flight.
+// A block streams up to rtb row tiles of one route chunk as one continuous step sequence
+// (the ring runs across tile boundaries; each tile ends with its epilogue). Only the stages
+// live in LDS: every wave derives the work item and its routes itself, so narrow tiles
+// (64 routes, one matrix) fit two blocks per CU.
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+template <int SIZE>
+DIH_DEV void to_lds(const void *src, void *lds_wave_base) {
+    if constexpr (SIZE == 16)
+        __builtin_amdgcn_global_load_lds((gbl_void_t *)src, (lds_void_t *)lds_wave_base, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((gbl_void_t *)src, (lds_void_t *)lds_wave_base, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding)
+template <int N>
+DIH_DEV void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+// Workgroup barrier without a memory fence: __syncthreads() would also wait for every
+// outstanding copy (the fence counts LDS copies as pending stores). Callers first wait
+// for their own copies of the step with wait_vm; the "memory" clobber keeps the compiler
+// from moving LDS accesses across the barrier.
+DIH_DEV void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+// Blocks per CU the streaming kernel is built for: two for the narrow route tiles (32 rows
+// of accumulators per matrix) when four stages fit in half the LDS; the VGPR budget is then
+// 256 per lane, accumulators included.
+template <int BITS, bool GATED, int NT>
+constexpr int qmm_lds_occupancy() {
+    return (GATED ? 2 : 1) * NT <= 2 &&
+                   4 * ((GATED ? 2 : 1) * 128 * (64 * BITS / 8) + 32 * NT * 128) <= 80 * 1024
+               ? 2 : 1;
+}
+
+template <int BITS, bool GATED, int NT, int S>
+__global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void qmm_lds_kernel(QmmParams P) {
+    constexpr int BN = 32 * NT;
+    constexpr int AB = 64 * BITS / 8;        // bytes of one row's codes per K step
+    constexpr int A_ST = 128 * AB;           // one matrix, one stage
+    constexpr int NMAT = GATED ? 2 : 1;
+    constexpr int B_ST = BN * 128;
+    constexpr int ST = NMAT * A_ST + B_ST;   // bytes per stage
+    constexpr int AQ = BITS == 8 ? 2 : 5;    // direct copies per wave per matrix per step
+    constexpr int LPS = NMAT * AQ + NT;      // copies per thread per step
+    static_assert(S == 4, "the stage of step s is s % 4, static within the eight-step unroll");
+    // one array per stage: with the stage known at compile time the compiler can tell that an
+    // operand read does not alias the copies in flight to the other stages. Nothing else
+    // lives in LDS, so that two blocks fit on a CU when the stages take half of it.
+    __shared__ __align__(16) unsigned char st0[ST], st1[ST], st2[ST], st3[ST];
+    auto stage_base = [&](int stage) -> unsigned char * {
+        return stage == 0 ? st0 : stage == 1 ? st1 : stage == 2 ? st2 : st3;
+    };
+
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    // ---- work item (every wave derives it): physical block b runs logical item
+    // L = (b % 8) * (grid / 8) + b / 8; L = chunk * rt_groups + row-tile group, a group
+    // being up to rtb consecutive row tiles
+    int e = 0, first = 0, nvalid = 0, rt0 = -1, nrt = 0;
+    {
+        const int b = blockIdx.x, per = (int)(gridDim.x >> 3);
+        const int L = (b & 7) * per + (b >> 3);
+        const int ci = L / P.rt_groups;
+        bool ok;
+        if (P.dense) {
+            ok = ci * BN < P.tokens;
+            if (ok) { first = ci * BN; nvalid = min(BN, P.tokens - first); }
+        } else {
+            int count;
+            const int total = chunk_of<BN>(P.counts, P.ngroups, ci, e, first, count);
+            ok = ci < total;
+            if (ok) nvalid = min(BN, count - first);
+        }
+        if (ok) {
+            rt0 = (L - ci * P.rt_groups) * P.rtb;
+            nrt = min(P.rtb, P.row_tiles - rt0);
+        }
+    }
+    if (rt0 < 0) return;
+    const int C = P.columns, R = P.rows, G = C >> 6;
+    const int total_steps = nrt * G;
+    // route of the chunk's n-th slot (slots past the chunk repeat its first route)
+    auto route_at = [&](int n) -> int {
+        n = n < nvalid ? n : 0;
+        return P.dense ? first + n : (int)P.routes[(size_t)e * P.tokens + first + n];
+    };
+
+    // ---- weights
+    const bool shared = !P.dense && e == P.experts;
+    const char *pw[2] = {reinterpret_cast<const char *>(shared ? P.sp0 : P.p0),
+                         reinterpret_cast<const char *>(shared ? P.sp1 : P.p1)};
+    const uint16_t *psc[2] = {shared ? P.ss0 : P.s0, shared ? P.ss1 : P.s1};
+    const uint16_t *pbi[2] = {shared ? P.sb0 : P.b0, shared ? P.sb1 : P.b1};
+    const size_t ebase = (size_t)(shared ? 0 : e) * R;
+    const size_t row_bytes = (size_t)C * BITS / 8;
+    auto row_index = [&](int rt, int rb) {  // (row tile, row in tile) -> matrix row (clamped)
+        const int row = rt * 128 + rb;
+        return ebase + (row < R ? row : R - 1);
+    };
+    // this lane's copy rows within a tile and byte offsets within a row's K-step segment
+    int crow[AQ], coff[AQ];
+#pragma unroll
+    for (int q = 0; q < AQ; q++) {
+        if constexpr (BITS == 8) {
+            const int rl = 16 * q + (lane >> 2), sl = lane & 3;
+            crow[q] = wave * 32 + rl;
+            coff[q] = 16 * (sl ^ ((rl >> 2) & 3));
+        } else {
+            const int i = 64 * q + lane, rl = i / 10;
+            crow[q] = wave * 32 + rl;
+            coff[q] = 4 * (i - rl * 10);
+        }
+    }
+    // this lane's MFMA row; its scale/bias bf16 bits come eight groups per 16-byte load
+    const int r = lane & 31, h = lane >> 5;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    auto win_load = [&](u32x4 (&sw)[2][2], int ti, int w) {
+        const size_t mrow = row_index(rt0 + ti, wave * 32 + r);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            sw[m][0] = *reinterpret_cast<const u32x4 *>(psc[m] + mrow * G + 8 * w);
+            sw[m][1] = *reinterpret_cast<const u32x4 *>(pbi[m] + mrow * G + 8 * w);
+        }
+    };
+
+    // ---- routes -> input row offsets of this lane's activation copies
+    const int T8 = P.tokens * 8;
+    const uint16_t *bsrc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+        const int n = (4 * i + wave) * 8 + (lane >> 3), sl = lane & 7;
+        const int route = route_at(n);
+        const int in_row = P.in_mode == 1 ? (route < T8 ? (route >> 3) : route - T8) : route;
+        bsrc[i] = P.x + (size_t)in_row * C + 8 * (sl ^ ((n >> 1) & 7));
+    }
+    // output routes of this lane's accumulator columns
+    int out_route[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) out_route[i] = route_at(32 * i + r);
+
+    // copies of flattened step s (row tile s / G, K step s % G) into `stage`
+    auto issue = [&](int step, int stage) {
+        step = step < total_steps ? step : total_steps - 1;
+        const int ti = step / G, kg = step - ti * G;
+        unsigned char *base = stage_base(stage);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+#pragma unroll
+            for (int q = 0; q < AQ; q++) {
+                const char *src = pw[m] + row_index(rt0 + ti, crow[q]) * row_bytes + (size_t)kg * AB + coff[q];
+                if constexpr (BITS == 8)
+                    to_lds<16>(src, base + m * A_ST + (wave * 32 + 16 * q) * 64);
+                else
+                    to_lds<4>(src, base + m * A_ST + wave * 32 * 40 + q * 256);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NT; i++) to_lds<16>(bsrc[i] + 64 * kg, base + NMAT * A_ST + (4 * i + wave) * 8 * 128);
+    };
+
+#pragma unroll
+    for (int st = 0; st < S - 1; st++) issue(st, st);
+    u32x4 win[2][2], win_next[2][2];
+    win_load(win, 0, 0);
+
+    dih_f32x16 acc0[NT], acc1[GATED ? NT : 1];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc0[i][k] = 0.f;
+        }
+        if constexpr (GATED) {
+#pragma unroll
+            for (int i = 0; i < NT; i++) {
+#pragma unroll
+                for (int k = 0; k < 16; k++) acc1[i][k] = 0.f;
+            }
+        }
+    };
+    zero_acc();
+
+    for (int ti = 0; ti < nrt; ti++) {
+        for (int kw = 0; kw < G; kw += 8) {
+            // the next window of scales: this tile's next one, or the next tile's first
+            const bool more = kw + 8 < G || ti + 1 < nrt;
+            if (more) win_load(win_next, kw + 8 < G ? ti : ti + 1, kw + 8 < G ? (kw >> 3) + 1 : 0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int step = ti * G + kw + u;
+                wait_vm<(S - 2) * LPS>();
+                barrier_no_fence();
+                issue(step + S - 1, (u + S - 1) % S);
+                const unsigned char *base = stage_base(u % S);
+                // this step's weights -> bf16 A operands
+                dih_bf16x8 a[2][4];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) {
+                    Chunk<BITS> c;
+                    if constexpr (BITS == 8) {
+                        const int sw = (r >> 2) & 3;
+                        const unsigned char *ra = base + m * A_ST + (wave * 32 + r) * 64;
+                        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(ra + 16 * ((2 * h) ^ sw));
+                        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(ra + 16 * ((2 * h + 1) ^ sw));
+                        c.w[0] = v0.x; c.w[1] = v0.y; c.w[2] = v0.z; c.w[3] = v0.w;
+                        c.w[4] = v1.x; c.w[5] = v1.y; c.w[6] = v1.z; c.w[7] = v1.w;
+                    } else {
+                        const uint32_t *ra = reinterpret_cast<const uint32_t *>(base + m * A_ST) + (wave * 32 + r) * 10 + 5 * h;
+#pragma unroll
+                        for (int k = 0; k < 5; k++) c.w[k] = ra[k];
+                    }
+                    const uint32_t sbits = (win[m][0][u >> 1] >> (16 * (u & 1))) & 0xffffu;
+                    const uint32_t bbits = (win[m][1][u >> 1] >> (16 * (u & 1))) & 0xffffu;
+                    chunk_to_bf16<BITS>(c, bf16_to_f32(sbits), bf16_to_f32(bbits), a[m]);
+                }
+                // MFMAs over all NT route tiles
+                const unsigned char *bb = base + NMAT * A_ST;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    dih_bf16x8 bx[NT];
+#pragma unroll
+                    for (int i = 0; i < NT; i++) {
+                        const int n = 32 * i + r, pc = 4 * h + j;
+                        bx[i] = *reinterpret_cast<const dih_bf16x8 *>(bb + n * 128 + 16 * (pc ^ ((n >> 1) & 7)));
+                    }
+#pragma unroll
+                    for (int i = 0; i < NT; i++) {
+                        acc0[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][j], bx[i], acc0[i], 0, 0, 0);
+                        if constexpr (GATED)
+                            acc1[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][j], bx[i], acc1[i], 0, 0, 0);
+                    }
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) { win[m][0] = win_next[m][0]; win[m][1] = win_next[m][1]; }
+            }
+        }
+
+        // ---- epilogue of row tile rt0 + ti: lane holds route n = 32i + r, rows
+        // 8*(k/4) + 4h + (k%4) of the wave's 32
+        const int row_base = (rt0 + ti) * 128 + wave * 32;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            const int n = 32 * i + r;
+            if (n >= nvalid) continue;
+            const int route = out_route[i];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int m0 = row_base + 8 * q + 4 * h;
+                float v[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float g = acc0[i][4 * q + k];
+                    if constexpr (GATED) v[k] = siluf_(g) * acc1[i][4 * q + k];
+                    else v[k] = g;
+                }
+                const size_t o = (size_t)route * R + m0;
+                if ((R & 3) == 0 && m0 + 3 < R) {
+                    if (P.y_bf16) {
+                        uint2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(P.y) + o) = pk;
+                    } else {
+                        *reinterpret_cast<float4 *>(static_cast<float *>(P.y) + o) = make_float4(v[0], v[1], v[2], v[3]);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        if (m0 + k < R) {
+                            if (P.y_bf16)
+                                static_cast<uint16_t *>(P.y)[o + k] = f32_to_bf16(v[k]);
+                            else
+                                static_cast<float *>(P.y)[o + k] = v[k];
+                        }
+                    }
+                }
+            }
+        }
+        zero_acc();
+    }
+    // no copy may still be writing this block's LDS when the block exits
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
 // Upper bound of (row tile, chunk) work items: sum_g ceil(count_g / BN) <= routes / BN +
 // (groups holding any route); a shared-expert group adds `tokens` routes.
 static size_t qmm_max_work(int rows, int tokens, int ngroups, int dense, int bn) {
@@ -351,10 +653,13 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         set_error(error, capacity, "Chunk too large for one grouped/dense qmm launch");
         return false;
     }
-    // Route tile width: 64 routes for the gated kernel, 128 otherwise (measured faster on
-    // every config than narrower tiles with deeper rings: occupancy hides more latency).
+    // Route tile width: 64 routes for the gated kernels, 128 otherwise (the register-ring
+    // kernel measured faster so than with narrower tiles and deeper rings). Grouped
+    // non-gated streaming launches (K a multiple of 512) use 64: experts average a few
+    // routes, and the narrower tile lets two blocks share a CU.
     const bool gated = m1 != nullptr;
-    const int nt = gated ? 2 : 4;
+    const bool streaming = m0->columns % 512 == 0;
+    const int nt = streaming && !a.dense && !gated ? 2 : (gated ? 2 : 4);
     const int bn = 32 * nt;
     const size_t work = qmm_max_work(m0->rows, a.tokens, a.ngroups, a.dense, bn);
     const size_t blocks = 8 * ((work + 7) / 8);
@@ -364,6 +669,26 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     }
     P.max_work = (int)work;
     dim3 grid((unsigned)blocks), block(256);
+    if (streaming) {
+        // row tiles per block: enough blocks to fill the GPU about twice, up to four tiles
+        // streamed back to back per block
+        const size_t chunks = work / (size_t)P.row_tiles;
+        const size_t per_tile = (size_t)P.row_tiles * chunks;
+        int rtb = (int)std::min<size_t>(4, std::max<size_t>(1, per_tile / 512));
+        rtb = std::min(rtb, P.row_tiles);
+        P.rtb = rtb;
+        P.rt_groups = (P.row_tiles + rtb - 1) / rtb;
+        const size_t lwork = chunks * (size_t)P.rt_groups;
+        grid = dim3((unsigned)(8 * ((lwork + 7) / 8)));
+#define DIH_QMM_LDS_CASE(B, GT, N)                                                  \
+        if (m0->bits == B && gated == GT && nt == N) {                              \
+            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4>), grid, block, 0, s, P);        \
+            return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
+        }
+        DIH_QMM_LDS_CASE(8, true, 2) DIH_QMM_LDS_CASE(8, false, 2) DIH_QMM_LDS_CASE(8, false, 4)
+        DIH_QMM_LDS_CASE(5, true, 2) DIH_QMM_LDS_CASE(5, false, 2) DIH_QMM_LDS_CASE(5, false, 4)
+#undef DIH_QMM_LDS_CASE
+    }
 #define DIH_QMM_CASE(B, GT, N, D)                                                   \
     if (m0->bits == B && gated == GT && nt == N) {                                  \
         DIH_LAUNCH((qmm_kernel<B, GT, N, D>), grid, block, 0, s, P);                \

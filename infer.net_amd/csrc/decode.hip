@@ -133,9 +133,90 @@ DIH_DEV float lane_x(float (&x)[32], const void *base, int x_bf16, const LaneGeo
     return s;
 }
 
-// (value desc, id asc): does candidate (va, ia) come before (vb, ib)?
+// Activations staged for the 8-bit f16 dot (chunk_dot_h8). Chunk c (32 columns) is stored
+// as f16 values x * 2^-k_c, with k_c = 0 unless the chunk's largest |x| reaches 2^15 (then
+// the scaled values stay below 2^15; a power-of-two scale is exact), as four 16-byte pieces
+// rotated by c/2 so that eight lanes reading eight chunks hit distinct bank groups. Per
+// chunk: the f32 sum of the stored f16 values (so that the 1024 offset cancels against
+// exactly the values the dot used) and 2^k_c.
+DIH_DEV int xh_at(int c, int p) { return c * 16 + 4 * ((p + (c >> 1)) & 3); }
+
+DIH_DEV void stage_xh_store(const uint4 v, int H, uint32_t *xh, float *xhs, float *xhm) {
+    const int t = threadIdx.x;
+    if (t < (H >> 3)) {
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        float f[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            f[2 * k] = __uint_as_float(u[k] << 16);
+            f[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+        }
+        // chunk maximum over its four staging threads; m < 2^e
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(f[i]));
+        m = fmaxf(m, dppf<DIH_DPP_XOR1>(m));
+        m = fmaxf(m, dppf<DIH_DPP_XOR2>(m));
+        const int e = (int)((__float_as_uint(m) >> 23) & 255u) - 126;
+        const int k = e > 15 ? e - 15 : 0;
+        uint32_t p[4];
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const _Float16 h0 = (_Float16)ldexpf(f[2 * i], -k), h1 = (_Float16)ldexpf(f[2 * i + 1], -k);
+            sum += (float)h0 + (float)h1;
+            p[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        }
+        const int c = t >> 2;
+        *reinterpret_cast<uint4 *>(&xh[xh_at(c, t & 3)]) = make_uint4(p[0], p[1], p[2], p[3]);
+        sum += dppf<DIH_DPP_XOR1>(sum);
+        sum += dppf<DIH_DPP_XOR2>(sum);
+        if ((t & 3) == 0) {
+            xhs[c] = sum;
+            xhm[c] = __uint_as_float((uint32_t)(127 + k) << 23);
+        }
+    }
+}
+
+// This lane's chunk of f16 activations; returns their sum, `mult` = 2^k of the chunk.
+DIH_DEV float lane_xh(uint32_t (&xr)[16], const uint32_t *xh, const float *xhs, const float *xhm,
+                      const LaneGeom &L, float &mult) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(&xh[xh_at(L.jc, p)]);
+        xr[4 * p] = v.x; xr[4 * p + 1] = v.y; xr[4 * p + 2] = v.z; xr[4 * p + 3] = v.w;
+    }
+    mult = xhm[L.jc];
+    return xhs[L.jc];
+}
+
+// rows_dot for 8-bit rows against f16-staged activations:
+// sum_i (q_i*s + b) * x_i = 2^k * (s * (sum_i (1024+q_i) x'_i - 1024 * xs') + b * xs').
+template <int NG>
+DIH_DEV void rows_dot_h8(const Rows<8, NG> &R, const uint32_t (&xr)[16], float xs, float mult, bool valid,
+                         int lpr, float (&out)[NG]) {
+#pragma unroll
+    for (int q = 0; q < NG; q++) {
+        const float d = chunk_dot_h8(R.w[q], xr) - 1024.f * xs;
+        const float v = mult * (bf16_to_f32(R.s[q]) * d + bf16_to_f32(R.b[q]) * xs);
+        out[q] = group_sum(valid ? v : 0.f, lpr);
+    }
+}
+
+// Sort key of a candidate: larger key = earlier in (value desc, id asc) order, with -0
+// equal to +0 (finite values; a non-finite router logit makes the step fail anyway).
+DIH_DEV unsigned long long rank_key(float v, uint32_t id) {
+    uint32_t u = __float_as_uint(v);
+    u = u == 0x80000000u ? 0u : u;
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (uint32_t)~id;
+}
+
+// (value desc, id asc): does candidate (va, ia) come before (vb, ib)? Bitwise, not
+// short-circuit: the logical form compiles to an exec-mask branch per comparison, which
+// made the 32-way rank take over a microsecond.
 DIH_DEV bool before(float va, uint32_t ia, float vb, uint32_t ib) {
-    return va > vb || (va == vb && ia < ib);
+    return (va > vb) | ((va == vb) & (ia < ib));
 }
 
 }  // namespace
@@ -171,7 +252,10 @@ template <int BITS>
 __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
     __shared__ __align__(16) float xl[2048];
     __shared__ float xsl[64];
+    __shared__ __align__(16) uint32_t xh[1024];
+    __shared__ float xhs[64], xhm[64];
     __shared__ __align__(16) float lg[kChunkExperts];
+    __shared__ __align__(16) unsigned long long lkey[kChunkExperts];
     const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     if (b < P.nchunks) {
@@ -183,50 +267,57 @@ __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
             const uint4 xv = stage_x_load(P.x, P.H);
             Rows<8, kRouterGroups> R;
             rows_load<8, kRouterGroups>(R, P.rp, P.rs, P.rb, 0, P.E, base, L.rpw, L.g, L.jc, P.H);
-            stage_x_store(xv, P.H, xl, xsl);
+            stage_xh_store(xv, P.H, xh, xhs, xhm);
             __syncthreads();
-            float x[32];
-            const float xs = lane_x_lds(x, xl, xsl, L);
+            uint32_t xr[16];
+            float mult;
+            const float xs = lane_xh(xr, xh, xhs, xhm, L, mult);
             float v[kRouterGroups];
-            rows_dot<8, kRouterGroups>(R, x, xs, L.valid, L.lpr, v);
+            rows_dot_h8<kRouterGroups>(R, xr, xs, mult, L.valid, L.lpr, v);
 #pragma unroll
             for (int q = 0; q < kRouterGroups; q++) {
                 const int o = wrow + q * L.rpw + L.g;  // row within the chunk
                 if (L.j == 0 && o < n) {
                     lg[o] = v[q];
-                    P.logits[b * kChunkExperts + o] = v[q];
+                    lkey[o] = rank_key(v[q], (uint32_t)(b * kChunkExperts + o));
                 }
             }
         } else if (threadIdx.x < kChunkExperts) {
             const int e = b * kChunkExperts + threadIdx.x;
             if ((int)threadIdx.x < n) {
                 lg[threadIdx.x] = P.logits_in[e];
-                P.logits[e] = P.logits_in[e];
+                lkey[threadIdx.x] = rank_key(lg[threadIdx.x], (uint32_t)e);
             }
         }
         // entries past the last expert rank after every real one
-        if (threadIdx.x < kChunkExperts && (int)threadIdx.x >= n) lg[threadIdx.x] = -INFINITY;
+        if (threadIdx.x < kChunkExperts && (int)threadIdx.x >= n) {
+            lg[threadIdx.x] = -INFINITY;
+            lkey[threadIdx.x] = rank_key(-INFINITY, 0xffffff00u + threadIdx.x);
+        }
         __syncthreads();
         if (wave == 0) {
-            // rank of each of the chunk's logits (all LDS reads independent broadcasts);
-            // the eight first become candidates
-            const bool mine = lane < n;
-            const float v = lane < kChunkExperts ? lg[lane] : -INFINITY;
-            const uint32_t id = mine ? (uint32_t)(b * kChunkExperts + lane) : 0xffffff00u + (uint32_t)lane;
-            const bool bad = __any(mine && !isfinite(v));
+            // rank of each of the chunk's logits: lane c and lane c + 32 each count the
+            // keys of one half of the chunk that order before candidate c (broadcast LDS
+            // reads, one 64-bit compare per key); the eight first become candidates
+            const int c = lane & 31, half = lane >> 5;
+            const unsigned long long me = lkey[c];
             int rank = 0;
 #pragma unroll
-            for (int k = 0; k < kChunkExperts; k += 4) {
-                const float4 q = *reinterpret_cast<const float4 *>(&lg[k]);
-                const float qv[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t ik = k + i < n ? (uint32_t)(b * kChunkExperts + k + i) : 0xffffff00u + (uint32_t)(k + i);
-                    rank += before(qv[i], ik, v, id) ? 1 : 0;
-                }
+            for (int k = 0; k < kChunkExperts / 2; k += 2) {
+                const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&lkey[half * (kChunkExperts / 2) + k]);
+                rank += q.x > me ? 1 : 0;
+                rank += q.y > me ? 1 : 0;
             }
+            rank += __shfl_xor(rank, 32, 64);
+            const bool mine = lane < n;
+            const float v = lg[c];
+            const uint32_t id = (uint32_t)(b * kChunkExperts + c);
+            const bool bad = __any(mine && !isfinite(v));
             if (lane < kChunkExperts && rank < 8)
-                P.cand[b * 8 + rank] = make_float2(v, __uint_as_float(bad ? 0xfffffffeu : id));
+                P.cand[b * 8 + rank] = make_float2(v, __uint_as_float(bad ? 0xfffffffeu : (lane < n ? id : 0xffffff00u + (uint32_t)c)));
+            // the logits go out after the barriers: a global store before a barrier would
+            // hold every wave until the store completes
+            if (mine) P.logits[b * kChunkExperts + lane] = v;
         }
         return;
     }
@@ -238,13 +329,23 @@ __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
         Rows<BITS, 1> G, U;
         rows_load<BITS, 1>(G, P.sgp, P.sgs, P.sgb, 0, P.I, base, L.rpw, L.g, L.jc, P.H);
         rows_load<BITS, 1>(U, P.sup, P.sus, P.sub, 0, P.I, base, L.rpw, L.g, L.jc, P.H);
-        stage_x_store(xv, P.H, xl, xsl);
-        __syncthreads();
-        float x[32];
-        const float xs = lane_x_lds(x, xl, xsl, L);
         float a[1], c[1];
-        rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
-        rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, c);
+        if constexpr (BITS == 8) {
+            stage_xh_store(xv, P.H, xh, xhs, xhm);
+            __syncthreads();
+            uint32_t xr[16];
+            float mult;
+            const float xs = lane_xh(xr, xh, xhs, xhm, L, mult);
+            rows_dot_h8<1>(G, xr, xs, mult, L.valid, L.lpr, a);
+            rows_dot_h8<1>(U, xr, xs, mult, L.valid, L.lpr, c);
+        } else {
+            stage_x_store(xv, P.H, xl, xsl);
+            __syncthreads();
+            float x[32];
+            const float xs = lane_x_lds(x, xl, xsl, L);
+            rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
+            rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, c);
+        }
         if (L.j == 0 && base + L.g < P.I) P.sact[base + L.g] = siluf_(a[0]) * c[0];
         return;
     }
@@ -264,8 +365,10 @@ __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
 
 template <int BITS>
 __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
-    __shared__ __align__(16) float xl[2048];
-    __shared__ float xsl[64];
+    __shared__ __align__(16) float xl[BITS == 8 ? 1 : 2048];
+    __shared__ float xsl[BITS == 8 ? 1 : 64];
+    __shared__ __align__(16) uint32_t xh[BITS == 8 ? 1024 : 1];
+    __shared__ float xhs[BITS == 8 ? 64 : 1], xhm[BITS == 8 ? 64 : 1];
     __shared__ __align__(16) float2 cl[64];
     __shared__ int rk[64];
     __shared__ uint32_t chosen[8];
@@ -284,7 +387,8 @@ __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
         rk[t] = 0;
         if (t == 0) any_bad = 0;
     }
-    stage_x_store(stage_x_load(P.x, P.H), P.H, xl, xsl);
+    if constexpr (BITS == 8) stage_xh_store(stage_x_load(P.x, P.H), P.H, xh, xhs, xhm);
+    else stage_x_store(stage_x_load(P.x, P.H), P.H, xl, xsl);
     __syncthreads();
     {
         const float2 me = cl[lane];
@@ -321,44 +425,79 @@ __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
         for (int s = 0; s < 8; s++) { P.ids[s] = bad ? 0u : chosen[s]; P.probs[s] = p[s] / total; }
         if (bad && P.status) *P.status = 1u;
     }
-    float x[32];
-    const float xs = lane_x_lds(x, xl, xsl, L);
     float a[1], u[1];
-    rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
-    rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, u);
+    if constexpr (BITS == 8) {
+        uint32_t xr[16];
+        float mult;
+        const float xs = lane_xh(xr, xh, xhs, xhm, L, mult);
+        rows_dot_h8<1>(G, xr, xs, mult, L.valid, L.lpr, a);
+        rows_dot_h8<1>(U, xr, xs, mult, L.valid, L.lpr, u);
+    } else {
+        float x[32];
+        const float xs = lane_x_lds(x, xl, xsl, L);
+        rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
+        rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, u);
+    }
     if (L.j == 0 && base + L.g < P.I) P.act[(size_t)slot * P.I + base + L.g] = siluf_(a[0]) * u[0];
 }
 
 // ------------------------------------------------------------------------------- K3
 
-template <int BITS>
+template <int BITS, int NV>
 __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
     __shared__ float part[9][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the nine activation rows (8 slots, then the shared expert) staged once per block as f32
+    // in the xl_at layout, row r at r*I, plus per-row chunk sums at 9*I + r*I/32
+    extern __shared__ __align__(16) float stage[];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int row0 = blockIdx.x * P.down_rows;
     const LaneGeom L = lane_geom(P.I, P.lpr_i);
-    // merge operands first (wave 0 lanes < down_rows merge)
-    float res = 0.f, route = 0.f, pr[8];
+    // merge operands first (wave 0 lanes < down_rows merge); the residual bits are loaded
+    // unconditionally and converted at the merge, so that no wait follows the load
     const int h = row0 + lane;
-    if (wave == 0) {
-        route = P.sroute[0];
+    const float route = P.sroute[0];
+    float pr[8];
 #pragma unroll
-        for (int s = 0; s < 8; s++) pr[s] = P.probs[s];
-        if (lane < P.down_rows && h < P.H) res = bf16_to_f32(P.residual[h]);
-    }
+    for (int s = 0; s < 8; s++) pr[s] = P.probs[s];
+    const uint32_t rbits = P.residual[h < P.H ? h : P.H - 1];
     const bool shared = wave == 8;
-    // activations first, then the expert id, then the weights that depend on it
-    float x[32];
-    const float *xa = shared ? P.sact : P.act + (size_t)wave * P.I;
-    load_x32(x, xa, 0, L.jc * 32);
-    const uint32_t e = shared ? 0u : P.ids[wave];
+    // activations first (NV coalesced float4 per thread), then the expert id (a
+    // wave-uniform scalar load, so waiting for it does not wait for the activations), then
+    // the weights that depend on it
+    const int n4 = 9 * (P.I >> 2), q4 = P.I >> 2;
+    float4 av[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        int i = t + 576 * k;
+        i = i < n4 ? i : n4 - 1;
+        const int slot = i / q4, f = i - slot * q4;
+        const float *src = slot < 8 ? P.act + (size_t)slot * P.I : P.sact;
+        av[k] = reinterpret_cast<const float4 *>(src)[f];
+    }
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t e = wv == 8 ? 0u : P.ids[wv];
     const uint32_t *wp = shared ? P.sdp : P.dp;
     const uint16_t *ws = shared ? P.sds : P.ds, *wb = shared ? P.sdb : P.db;
     Rows<BITS, kDownGroups> R;
     rows_load<BITS, kDownGroups>(R, wp, ws, wb, (size_t)e * P.H, P.H, row0, L.rpw, L.g, L.jc, P.I);
-    float xs = 0.f;
+    // staging: eight consecutive threads hold the eight float4 of one 32-value chunk
+    float *xsums = stage + 9 * P.I;
 #pragma unroll
-    for (int i = 0; i < 32; i++) xs += x[i];
+    for (int k = 0; k < NV; k++) {
+        const int i = t + 576 * k;
+        float sum = (av[k].x + av[k].y) + (av[k].z + av[k].w);
+        sum += dppf<DIH_DPP_XOR1>(sum);
+        sum += dppf<DIH_DPP_XOR2>(sum);
+        sum += dppf<DIH_DPP_HALF_MIRROR>(sum);
+        if (i < n4) {
+            const int slot = i / q4, f = i - slot * q4, c = f >> 3;
+            *reinterpret_cast<float4 *>(&stage[slot * P.I + xl_at(c, 4 * (f & 7))]) = av[k];
+            if ((f & 7) == 0) xsums[slot * (P.I >> 5) + c] = sum;
+        }
+    }
+    __syncthreads();
+    float x[32];
+    const float xs = lane_x_lds(x, stage + wave * P.I, xsums + wave * (P.I >> 5), L);
     float v[kDownGroups];
     rows_dot<BITS, kDownGroups>(R, x, xs, L.valid, L.lpr, v);
 #pragma unroll
@@ -370,7 +509,7 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
         float y = sh * sigmoidf_(route);
 #pragma unroll
         for (int s = 0; s < 8; s++) y += part[s][lane] * pr[s];
-        P.residual[h] = f32_to_bf16(res + y);
+        P.residual[h] = f32_to_bf16(bf16_to_f32(rbits) + y);
         if (P.route_out) {
 #pragma unroll
             for (int s = 0; s < 8; s++) P.route_out[(size_t)s * P.H + h] = part[s][lane];
@@ -392,7 +531,7 @@ bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix 
     const int E = gate->experts, H = gate->columns, I = gate->rows;
     return (!router || router->bits == 8) && sr->bits == 8 && sg->bits == gate->bits &&
            sd->bits == gate->bits && down->bits == gate->bits && sg->rows == I && sd->columns == I &&
-           H <= 2048 && I <= 2048 && E <= 256 && (gate->bits == 8 || gate->bits == 5);
+           H <= 2048 && I <= 1024 && E <= 256 && (gate->bits == 8 || gate->bits == 5);
 }
 
 bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int capacity) {
@@ -423,20 +562,29 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
     const int k1 = P.nchunks + P.shared_blocks + 1;
     const int k2 = 8 * P.gate_blocks;
     const int k3 = (P.H + P.down_rows - 1) / P.down_rows;
+    const size_t k3_lds = (size_t)9 * P.I * 4 + (size_t)9 * (P.I / 32) * 4;
     if (gate->bits == 8) {
         prof_stage("decode_router_shared");
         DIH_LAUNCH(decode_router_kernel<8>, dim3(k1), dim3(1024), 0, s, P);
         prof_stage("decode_experts_gate_up");
         DIH_LAUNCH(decode_experts_kernel<8>, dim3(k2), dim3(1024), 0, s, P);
         prof_stage("decode_down_merge");
-        DIH_LAUNCH(decode_down_kernel<8>, dim3(k3), dim3(576), 0, s, P);
+        // float4 activation loads per K3 thread: 9 rows of I floats over 576 threads
+        // (I <= 1024: at most four; the staged rows then take at most 37 KB of LDS)
+        const int nv = (9 * (P.I / 4) + 575) / 576;
+        if (nv <= 1) DIH_LAUNCH((decode_down_kernel<8, 1>), dim3(k3), dim3(576), k3_lds, s, P);
+        else if (nv <= 2) DIH_LAUNCH((decode_down_kernel<8, 2>), dim3(k3), dim3(576), k3_lds, s, P);
+        else DIH_LAUNCH((decode_down_kernel<8, 4>), dim3(k3), dim3(576), k3_lds, s, P);
     } else {
         prof_stage("decode_router_shared");
         DIH_LAUNCH(decode_router_kernel<5>, dim3(k1), dim3(1024), 0, s, P);
         prof_stage("decode_experts_gate_up");
         DIH_LAUNCH(decode_experts_kernel<5>, dim3(k2), dim3(1024), 0, s, P);
         prof_stage("decode_down_merge");
-        DIH_LAUNCH(decode_down_kernel<5>, dim3(k3), dim3(576), 0, s, P);
+        const int nv = (9 * (P.I / 4) + 575) / 576;
+        if (nv <= 1) DIH_LAUNCH((decode_down_kernel<5, 1>), dim3(k3), dim3(576), k3_lds, s, P);
+        else if (nv <= 2) DIH_LAUNCH((decode_down_kernel<5, 2>), dim3(k3), dim3(576), k3_lds, s, P);
+        else DIH_LAUNCH((decode_down_kernel<5, 4>), dim3(k3), dim3(576), k3_lds, s, P);
     }
     return hip_ok(hipGetLastError(), error, capacity, "decode MoE launch");
 }

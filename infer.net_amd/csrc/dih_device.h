@@ -77,6 +77,25 @@ DIH_DEV float chunk_dot(const Chunk<BITS> &c, const float *x) {
     return (a0 + a1) + (a2 + a3);
 }
 
+// 8-bit codes against f16 activations, two codes per instruction: v_perm_b32 turns bytes
+// q0..q3 of a code word into the f16 pairs (1024+q0, 1024+q1) and (1024+q2, 1024+q3)
+// (0x64 is the high byte of f16 1024.0, whose unit in the last place is 1, so 1024+q is
+// exact), and v_dot2_f32_f16 accumulates pair . (x_i, x_i+1) in f32. Returns
+// sum_i (1024 + q_i) * x_i; the caller subtracts 1024 * sum_i x_i. xh holds the chunk's 32
+// activations as 16 f16 pairs.
+typedef _Float16 dih_half2 __attribute__((ext_vector_type(2)));
+DIH_DEV float chunk_dot_h8(const Chunk<8> &c, const uint32_t (&xh)[16]) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, c.w[w], 0x04010400u);
+        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, c.w[w], 0x04030402u);
+        a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(dih_half2, lo), __builtin_bit_cast(dih_half2, xh[2 * w]), a0, false);
+        a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(dih_half2, hi), __builtin_bit_cast(dih_half2, xh[2 * w + 1]), a1, false);
+    }
+    return a0 + a1;
+}
+
 // Dequantize a chunk to bf16 MFMA operands: operand j holds codes 8j..8j+7 as
 // bf16(code*scale + bias) with the fp32 value rounded to nearest even (the reference's
 // bfloat(float(q)*scale+bias), prefill_expert_packed.mm:34).

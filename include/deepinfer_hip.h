@@ -219,6 +219,62 @@ int dih_set_profiling(void *context, int enabled);
 int dih_profile_read(void *context, double *total_ms, int *counts, const char **names,
                      int capacity);
 
+/* ---- Checkpoint loading (host code; no GPU work except the uploads of dih_checkpoint_*) ----
+ * Status codes of this group: 0 ok, -1 invalid data (the reference's InvalidDataException),
+ * -2 unsupported (NotSupportedException); the message text is the reference's. */
+
+/* Safetensors reader (SafeTensors.cs:13-44): validates the header (u64 LE length in
+ * [2, 16 MiB] and inside the file; dtypes BF16/F32/U32 only, else -2; rank 1..8, dims >= 1;
+ * data_offsets inside the data section with end-begin = elements*dtype size; no duplicate
+ * names; no overlapping ranges). `status` (optional) receives the code. */
+void *dih_safetensors_open(const char *path, int *status, char *error, int capacity);
+void dih_safetensors_close(void *file);
+/* Number of tensors, and tensor `index` in header order: dtype 1 BF16, 2 F32, 3 U32;
+ * shape[rank] (rank <= 8); byte length. */
+int dih_safetensors_count(void *file);
+int dih_safetensors_info(void *file, int index, char *name, int name_capacity, int *dtype,
+                         int *rank, int64_t *shape, uint64_t *bytes);
+/* SafeTensors.Get (SafeTensors.cs:45-50): 0 when `name` exists with exactly this shape,
+ * else -1 "Missing tensor or shape mismatch: NAME." */
+int dih_safetensors_get(void *file, const char *name, const int64_t *shape, int rank,
+                        char *error, int capacity);
+/* SafeTensors.ReadInto (SafeTensors.cs:57-63) into host memory; `bytes` must equal the
+ * tensor's byte length. dtype 1 (BF16) additionally requires a BF16 tensor
+ * (ReadBFloat16, SafeTensors.cs:51-56); dtype 0 accepts any. */
+int dih_safetensors_read(void *file, const char *name, int dtype, void *destination,
+                         uint64_t bytes, char *error, int capacity);
+/* SafeTensors.ReadFloat (SafeTensors.cs:64-80): F32 as stored or BF16 widened to f32;
+ * `count` must equal the element count; any non-finite value fails. */
+int dih_safetensors_read_float(void *file, const char *name, float *destination,
+                               uint64_t count, char *error, int capacity);
+
+/* MLX checkpoint directory (Qwen36Weights.cs:26-65): config.json must describe the
+ * Qwen3.6-35B-A3B text geometry, unscaled RoPE, affine group-64 5- or 8-bit quantization;
+ * model.safetensors.index.json maps tensors to shard files (plain file names only). Shards
+ * open on first use. */
+void *dih_checkpoint_open(const char *directory, int *status, char *error, int capacity);
+void dih_checkpoint_close(void *checkpoint);
+int dih_checkpoint_info(void *checkpoint, int *bits, float *epsilon, float *rope_theta);
+/* Qwen36Weights.Matrix (Qwen36Weights.cs:66-81): tensors PREFIX.weight (U32
+ * [experts,] rows, columns*bits/32), PREFIX.scales and PREFIX.biases (BF16 [experts,]
+ * rows, columns/64); experts == 1 means no leading expert dimension; bits 0 = the
+ * checkpoint's; a per-prefix quantization override must agree. Returns a matrix handle
+ * (free with dih_quant_matrix_destroy) whose device buffers hold the tensor bytes, streamed
+ * through pinned staging (the reference reads into unified memory, QuantizedMetal.cs:177). */
+void *dih_checkpoint_matrix(void *checkpoint, void *context, const char *prefix, int rows,
+                            int columns, int experts, int bits, int *status, char *error,
+                            int capacity);
+/* Qwen36Weights.Vector (Qwen36Weights.cs:82): ReadFloat of a tensor of exactly `shape`. */
+int dih_checkpoint_vector(void *checkpoint, const char *name, const int64_t *shape, int rank,
+                          float *destination, uint64_t count, char *error, int capacity);
+/* The eight MoE matrices of decoder layer `layer` (Qwen36Weights.cs:90-99): router
+ * mlp.gate [256, 2048] 8-bit, mlp.switch_mlp.{gate,up}_proj [256, 512, 2048],
+ * mlp.switch_mlp.down_proj [256, 2048, 512], mlp.shared_expert.{gate,up}_proj [512, 2048],
+ * mlp.shared_expert.down_proj [2048, 512], mlp.shared_expert_gate [1, 2048] 8-bit. On
+ * failure no matrix is left allocated. */
+int dih_checkpoint_moe_layer(void *checkpoint, void *context, int layer, dih_moe_layer *out,
+                             char *error, int capacity);
+
 /* Library build string (kernels' target and version). */
 const char *dih_version(void);
 

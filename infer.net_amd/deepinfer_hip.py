@@ -46,6 +46,14 @@ class InvalidOperationError(RuntimeError):
     """System.InvalidOperationException"""
 
 
+class InvalidDataError(ValueError):
+    """System.IO.InvalidDataException (checkpoint and safetensors validation)"""
+
+
+class NotSupportedError(Exception):
+    """System.NotSupportedException (unsupported dtype, geometry or quantization)"""
+
+
 class Job(ctypes.Structure):
     _fields_ = [("matrix", ctypes.c_void_p), ("input", ctypes.c_void_p),
                 ("output", ctypes.c_void_p), ("experts", ctypes.c_void_p),
@@ -70,6 +78,11 @@ EXPORTS = [
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
     "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_dense", "dih_set_profiling",
     "dih_profile_read", "dih_version",
+    "dih_safetensors_open", "dih_safetensors_close", "dih_safetensors_count",
+    "dih_safetensors_info", "dih_safetensors_get", "dih_safetensors_read",
+    "dih_safetensors_read_float", "dih_checkpoint_open", "dih_checkpoint_close",
+    "dih_checkpoint_info", "dih_checkpoint_matrix", "dih_checkpoint_vector",
+    "dih_checkpoint_moe_layer",
 ]
 
 _lib = None
@@ -116,6 +129,19 @@ def load():
         "dih_set_profiling": ([P, I], I),
         "dih_profile_read": ([P, P, P, P, I], I),
         "dih_version": ([], ctypes.c_char_p),
+        "dih_safetensors_open": ([E, P, E, I], P),
+        "dih_safetensors_close": ([P], None),
+        "dih_safetensors_count": ([P], I),
+        "dih_safetensors_info": ([P, I, E, I, P, P, P, P], I),
+        "dih_safetensors_get": ([P, E, P, I, E, I], I),
+        "dih_safetensors_read": ([P, E, I, P, ctypes.c_uint64, E, I], I),
+        "dih_safetensors_read_float": ([P, E, P, ctypes.c_uint64, E, I], I),
+        "dih_checkpoint_open": ([E, P, E, I], P),
+        "dih_checkpoint_close": ([P], None),
+        "dih_checkpoint_info": ([P, P, P, P], I),
+        "dih_checkpoint_matrix": ([P, P, E, I, I, I, I, P, E, I], P),
+        "dih_checkpoint_vector": ([P, E, P, I, P, ctypes.c_uint64, E, I], I),
+        "dih_checkpoint_moe_layer": ([P, P, I, P, E, I], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -518,6 +544,196 @@ def profile_read(dev):
     if n < 0:
         raise InvalidOperationError("profile read failed")
     return {names[i].decode(): (ms[i], counts[i]) for i in range(n)}
+
+
+# ---------------------------------------------------------------------------------------
+# Checkpoint loading: SafeTensors (SafeTensors.cs) and the MLX checkpoint directory
+# (Qwen36Weights.cs), backed by the library's native reader and uploader.
+
+_DTYPES = {1: "BF16", 2: "F32", 3: "U32"}
+
+
+def _st_raise(code, buf):
+    if code == -2:
+        raise NotSupportedError(_msg(buf))
+    raise InvalidDataError(_msg(buf))
+
+
+def _enc(s: str) -> bytes:
+    return s.encode("utf-8")
+
+
+class SafeTensors:
+    """Mirror of SafeTensors (SafeTensors.cs:7-95): a validated header and typed reads."""
+
+    class Tensor:
+        __slots__ = ("name", "dtype", "shape", "bytes", "_owner")
+
+        def __init__(self, name, dtype, shape, nbytes, owner):
+            self.name, self.dtype, self.shape, self.bytes, self._owner = name, dtype, tuple(shape), nbytes, owner
+
+        def __repr__(self):
+            return f"Tensor({self.name!r}, {self.dtype}, {list(self.shape)}, {self.bytes})"
+
+    def __init__(self, path: str):
+        L = load()
+        err, st = _errbuf(), ctypes.c_int(0)
+        h = L.dih_safetensors_open(_enc(os.fspath(path)), ctypes.byref(st), err, _ERR)
+        if not h:
+            _st_raise(st.value, err)
+        self._h = h
+        self._tensors = {}
+        name = ctypes.create_string_buffer(4096)
+        dt, rank = ctypes.c_int(), ctypes.c_int()
+        shape = (ctypes.c_int64 * 8)()
+        nbytes = ctypes.c_uint64()
+        for i in range(L.dih_safetensors_count(h)):
+            if L.dih_safetensors_info(h, i, name, 4096, ctypes.byref(dt), ctypes.byref(rank), shape,
+                                      ctypes.byref(nbytes)) != 0:
+                raise InvalidDataError("Invalid tensor entry.")
+            n = name.value.decode("utf-8")
+            self._tensors[n] = SafeTensors.Tensor(n, _DTYPES[dt.value], list(shape[:rank.value]),
+                                                  nbytes.value, self)
+
+    def _alive(self):
+        if not self._h:
+            raise ObjectDisposedError("SafeTensors")
+
+    @property
+    def tensors(self):
+        return dict(self._tensors)
+
+    def get(self, name: str, *shape: int) -> "SafeTensors.Tensor":
+        self._alive()
+        err = _errbuf()
+        arr = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+        rc = load().dih_safetensors_get(self._h, _enc(name), arr, len(shape), err, _ERR)
+        if rc != 0:
+            _st_raise(rc, err)
+        return self._tensors[name]
+
+    def _own(self, tensor):
+        if not isinstance(tensor, SafeTensors.Tensor) or tensor._owner is not self:
+            raise InvalidDataError("Tensor ownership or destination length mismatch.")
+
+    def read_into(self, tensor: "SafeTensors.Tensor", destination: np.ndarray) -> None:
+        self._alive()
+        self._own(tensor)
+        if not (isinstance(destination, np.ndarray) and destination.flags.c_contiguous):
+            raise InvalidDataError("Tensor ownership or destination length mismatch.")
+        err = _errbuf()
+        rc = load().dih_safetensors_read(self._h, _enc(tensor.name), 0, destination.ctypes.data,
+                                         destination.nbytes, err, _ERR)
+        if rc != 0:
+            _st_raise(rc, err)
+
+    def read_bfloat16(self, tensor: "SafeTensors.Tensor") -> np.ndarray:
+        self._alive()
+        self._own(tensor)
+        out = np.empty(tensor.bytes // 2, dtype=np.uint16)
+        err = _errbuf()
+        rc = load().dih_safetensors_read(self._h, _enc(tensor.name), 1, out.ctypes.data, out.nbytes, err, _ERR)
+        if rc != 0:
+            _st_raise(rc, err)
+        return out
+
+    def read_float(self, tensor: "SafeTensors.Tensor") -> np.ndarray:
+        self._alive()
+        self._own(tensor)
+        n = tensor.bytes // (2 if tensor.dtype == "BF16" else 4)
+        out = np.empty(n, dtype=np.float32)
+        err = _errbuf()
+        rc = load().dih_safetensors_read_float(self._h, _enc(tensor.name), out.ctypes.data, n, err, _ERR)
+        if rc != 0:
+            _st_raise(rc, err)
+        return out
+
+    def dispose(self) -> None:
+        if self._h:
+            load().dih_safetensors_close(self._h)
+            self._h = None
+
+    close = dispose
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.dispose()
+
+
+class Checkpoint:
+    """The MLX checkpoint directory of Qwen36Weights (Qwen36Weights.cs:26-122): validated
+    config, shard index, and matrices loaded straight into device memory."""
+
+    def __init__(self, directory: str):
+        L = load()
+        err, st = _errbuf(), ctypes.c_int(0)
+        h = L.dih_checkpoint_open(_enc(os.fspath(directory)), ctypes.byref(st), err, _ERR)
+        if not h:
+            _st_raise(st.value, err)
+        self._h = h
+        bits, eps, theta = ctypes.c_int(), ctypes.c_float(), ctypes.c_float()
+        L.dih_checkpoint_info(h, ctypes.byref(bits), ctypes.byref(eps), ctypes.byref(theta))
+        self.weight_bits, self.epsilon, self.rope_theta = bits.value, eps.value, theta.value
+
+    def _alive(self):
+        if not self._h:
+            raise ObjectDisposedError("Checkpoint")
+
+    def matrix(self, device: QuantizedHip, prefix: str, rows: int, columns: int, experts: int = 1,
+               bits: int = 0) -> QuantMatrix:
+        """Qwen36Weights.Matrix: PREFIX.{weight,scales,biases} -> a device-resident matrix."""
+        self._alive()
+        device._alive()
+        err, st = _errbuf(), ctypes.c_int(0)
+        h = load().dih_checkpoint_matrix(self._h, device.context, _enc(prefix), rows, columns, experts, bits,
+                                         ctypes.byref(st), err, _ERR)
+        if not h:
+            _st_raise(st.value, err)
+        return QuantMatrix(device, h, experts, rows, columns, bits or self.weight_bits)
+
+    def vector(self, name: str, *shape: int) -> np.ndarray:
+        """Qwen36Weights.Vector: ReadFloat of a tensor of exactly `shape`."""
+        self._alive()
+        n = int(np.prod(shape)) if shape else 0
+        out = np.empty(n, dtype=np.float32)
+        err = _errbuf()
+        arr = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+        rc = load().dih_checkpoint_vector(self._h, _enc(name), arr, len(shape), out.ctypes.data, n, err, _ERR)
+        if rc != 0:
+            _st_raise(rc, err)
+        return out
+
+    def moe_layer(self, device: QuantizedHip, layer: int):
+        """The eight MoE matrices of decoder layer `layer` (Qwen36Weights.cs:90-99); returns
+        (MoeLayer for moe_decode/moe_prefill, [QuantMatrix] owning them)."""
+        self._alive()
+        device._alive()
+        out, err = MoeLayer(), _errbuf()
+        rc = load().dih_checkpoint_moe_layer(self._h, device.context, layer, ctypes.byref(out), err, _ERR)
+        if rc != 0:
+            _st_raise(rc, err)
+        b = self.weight_bits
+        shapes = [(256, 2048, 1, 8), (512, 2048, 256, b), (512, 2048, 256, b), (2048, 512, 256, b),
+                  (512, 2048, 1, b), (512, 2048, 1, b), (2048, 512, 1, b), (1, 2048, 1, 8)]
+        handles = [out.router, out.gate, out.up, out.down, out.shared_gate, out.shared_up,
+                   out.shared_down, out.shared_route]
+        mats = [QuantMatrix(device, h, e, r, c, bb) for h, (r, c, e, bb) in zip(handles, shapes)]
+        return out, mats
+
+    def dispose(self) -> None:
+        if self._h:
+            load().dih_checkpoint_close(self._h)
+            self._h = None
+
+    close = dispose
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.dispose()
 
 
 def version() -> str:

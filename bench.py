@@ -321,6 +321,48 @@ class Bench:
         torch.cuda.synchronize()
         return {"bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": steps}
 
+    def load(self, reps=3):
+        """Checkpoint loading (dih_checkpoint_moe_layer): one config-2 MoE layer written in the
+        MLX safetensors layout to a temporary directory (so the shard files sit in the page
+        cache), then loaded `reps` times into device matrices. Reports file -> HBM GB/s."""
+        import shutil
+        import tempfile
+        import numpy as np
+        sys.path.insert(0, ROOT)
+        from tests import ckpt_util as cu
+        dh = self.dh
+        rng = np.random.default_rng(0)
+        d = tempfile.mkdtemp(prefix="dih-load-")
+        try:
+            p = "language_model.model.layers.0."
+            spec = [("mlp.gate", 1, E, H, 8), ("mlp.switch_mlp.gate_proj", E, I, H, 8),
+                    ("mlp.switch_mlp.up_proj", E, I, H, 8), ("mlp.switch_mlp.down_proj", E, H, I, 8),
+                    ("mlp.shared_expert.gate_proj", 1, I, H, 8), ("mlp.shared_expert.up_proj", 1, I, H, 8),
+                    ("mlp.shared_expert.down_proj", 1, H, I, 8), ("mlp.shared_expert_gate", 1, 1, H, 8)]
+            t, total = {}, 0
+            for name, e, r, c, bits in spec:
+                lead = () if e == 1 else (e,)
+                w = rng.integers(0, 1 << 32, size=lead + (r, c * bits // 32), dtype=np.uint32)
+                sc = np.full(lead + (r, c // 64), 0x3a80, dtype=np.uint16)
+                bi = np.full(lead + (r, c // 64), 0xbf00, dtype=np.uint16)
+                t.update(cu.matrix_tensors(p + name, w, sc, bi))
+                total += w.nbytes + sc.nbytes + bi.nbytes
+            cu.write_checkpoint(d, t, bits=8, shards=2)
+            del t
+            times = []
+            for _ in range(reps + 1):
+                t0 = time.perf_counter()
+                with dh.Checkpoint(d) as ck:
+                    _, mats = ck.moe_layer(self.dev, 0)
+                times.append(time.perf_counter() - t0)
+                for m in mats:
+                    m.dispose()
+            best = min(times[1:])
+            return {"bytes": total, "ms": best * 1e3, "GB_s": total / best / 1e9,
+                    "note": "shard files in the page cache; pread -> 2x64 MiB pinned staging -> H2D"}
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+
     def free(self, built):
         for mats, _ in built:
             for m in mats.values():
@@ -394,6 +436,9 @@ def main():
     if on("dense"):
         res["dense"] = b.dense(steps, warmup)
         log(f"[dense] {res['dense']['TFLOP_s']:.1f} TFLOP/s")
+    if "load" in wls:
+        res["load"] = b.load()
+        log(f"[load] {res['load']['GB_s']:.1f} GB/s ({res['load']['bytes'] / 1e6:.0f} MB in {res['load']['ms']:.1f} ms)")
     if "copycal" in wls:
         print(json.dumps(b.copycal(max(1, min(steps, 8)))), flush=True)
         return

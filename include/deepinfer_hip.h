@@ -192,6 +192,27 @@ int dih_moe_decode(void *context, const dih_moe_layer *layer, const void *x,
                    const float *logits, void *residual, const dih_moe_trace *trace,
                    void *stream, char *error, int capacity);
 
+/* Residual storage and next-layer norm for the MoE steps (graph_merge_norm,
+ * gpu_graph.mm:48-61; prefill_merge, gpu_prefill.mm:140-150). residual_f32 = 1 keeps the
+ * residual stream in f32 like the reference (0: bf16 bit patterns). With norm_weight
+ * (f32 [H]) the step also writes normed[t] = r[t] * rsqrt(sum_h r[t][h]^2 / H + epsilon) *
+ * norm_weight over the stored residual r (f32 when normed_f32 = 1, else bf16); epsilon must be
+ * finite and > 0 (Qwen36Weights.cs:51) and normed must not be the residual buffer. */
+typedef struct dih_moe_merge {
+    int residual_f32;
+    const float *norm_weight;
+    float epsilon;
+    void *normed;
+    int normed_f32;
+} dih_moe_merge;
+
+/* dih_moe_decode with merge options (NULL: bf16 residual, no norm). The norm is one more
+ * single-block launch after the merge (every output row must be final before the sum of
+ * squares). */
+int dih_moe_decode_norm(void *context, const dih_moe_layer *layer, const void *x,
+                        const float *logits, void *residual, const dih_moe_merge *merge,
+                        const dih_moe_trace *trace, void *stream, char *error, int capacity);
+
 /* Prefill MoE chunk (gpu_prefill.mm:700-706 with packed_expert_gate_fused /
  * packed_expert_down, prefill_expert_packed.mm, and prefill_merge gpu_prefill.mm:140-150):
  * top-8 of logits (bf16 or f32 [T][E]) -> grouped per-expert route lists -> bf16 MFMA
@@ -202,6 +223,13 @@ int dih_moe_decode(void *context, const dih_moe_layer *layer, const void *x,
 int dih_moe_prefill(void *context, const dih_moe_layer *layer, int tokens, const void *x,
                     const void *logits, int logits_dtype, void *residual,
                     const dih_moe_trace *trace, void *stream, char *error, int capacity);
+
+/* dih_moe_prefill with merge options (NULL: bf16 residual, no norm); the norm is fused into
+ * the per-token merge (prefill_merge, gpu_prefill.mm:140-150). */
+int dih_moe_prefill_norm(void *context, const dih_moe_layer *layer, int tokens, const void *x,
+                         const void *logits, int logits_dtype, void *residual,
+                         const dih_moe_merge *merge, const dih_moe_trace *trace, void *stream,
+                         char *error, int capacity);
 
 /* Dense batched projection through the same MFMA qmm (p_gemv dense path,
  * gpu_prefill.mm:603-614, prefill_bf16.mm:7-53): Y[t][r] = sum_c w(0,r,c)*X[t][c],

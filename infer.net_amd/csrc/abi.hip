@@ -3,6 +3,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <new>
 #include <string>
 
@@ -679,16 +680,43 @@ static bool check_layer(Context *c, const dih_moe_layer *L, bool need_router, in
     return true;
 }
 
+// dih_moe_merge -> MergeOut, validated (NULL = bf16 residual, no norm)
+static bool merge_of(const dih_moe_merge *m, const void *residual, MergeOut &mo, char *error, int capacity) {
+    mo = MergeOut();
+    if (!m) return true;
+    if ((m->residual_f32 != 0 && m->residual_f32 != 1) || (m->normed_f32 != 0 && m->normed_f32 != 1) ||
+        (m->norm_weight && (!m->normed || m->normed == residual || !std::isfinite(m->epsilon) || m->epsilon <= 0.f))) {
+        set_error(error, capacity, "Invalid MoE merge options");
+        return false;
+    }
+    mo.residual_f32 = m->residual_f32;
+    mo.norm_w = m->norm_weight;
+    mo.eps = m->epsilon;
+    mo.normed = m->normed;
+    mo.normed_f32 = m->normed_f32;
+    return true;
+}
+
 __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_moe_layer *L, const void *x,
                                                           const float *logits, void *residual,
                                                           const dih_moe_trace *trace, void *stream, char *error,
                                                           int capacity) {
+    return dih_moe_decode_norm(ctx, L, x, logits, residual, nullptr, trace, stream, error, capacity);
+}
+
+__attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const dih_moe_layer *L, const void *x,
+                                                               const float *logits, void *residual,
+                                                               const dih_moe_merge *merge,
+                                                               const dih_moe_trace *trace, void *stream,
+                                                               char *error, int capacity) {
     Context *c = as_ctx(ctx);
     int E, H, I, Is;
+    MergeOut mo;
     if (!c || !x || !residual) {
         set_error(error, capacity, "Invalid decode MoE arguments");
         return -1;
     }
+    if (!merge_of(merge, residual, mo, error, capacity)) return -1;
     if (!check_layer(c, L, logits == nullptr, &E, &H, &I, &Is, error, capacity)) return -1;
     if (logits && L->router) {
         set_error(error, capacity, "Pass either a router matrix or logits, not both");
@@ -722,9 +750,15 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
         a.probs = trace && trace->probs ? trace->probs : probs;
         a.status = trace ? trace->status : nullptr;
         a.x = static_cast<const uint16_t *>(x);
-        a.residual = static_cast<uint16_t *>(residual);
+        a.residual = residual;
+        a.residual_f32 = mo.residual_f32;
         a.route_out = trace ? trace->expert_out : nullptr;
-        const bool ok = launch_moe_decode(a, s, error, capacity);
+        bool ok = launch_moe_decode(a, s, error, capacity);
+        if (ok && mo.norm_w) {
+            prof_stage("decode_norm");
+            ok = launch_rmsnorm(residual, mo.residual_f32, 1, H, mo.norm_w, mo.eps, mo.normed, mo.normed_f32, s, error,
+                                capacity);
+        }
         prof_stage("kernel");
         return ok ? 0 : -1;
     }
@@ -770,10 +804,16 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
     }
     prof_mark(c, s, "decode_experts_gate_up");
     // Stage 3: expert down projections and the weighted merge into the residual.
-    if (!launch_moe_down_merge(down, act, ids, probs, sout, srt, static_cast<uint16_t *>(residual),
+    if (!launch_moe_down_merge(down, act, ids, probs, sout, srt, residual, mo.residual_f32,
                                trace ? trace->expert_out : nullptr, s, error, capacity))
         return -1;
     prof_mark(c, s, "decode_down_merge");
+    if (mo.norm_w) {
+        if (!launch_rmsnorm(residual, mo.residual_f32, 1, H, mo.norm_w, mo.eps, mo.normed, mo.normed_f32, s, error,
+                            capacity))
+            return -1;
+        prof_mark(c, s, "decode_norm");
+    }
     if (trace) {
         if (trace->logits && !hip_ok(hipMemcpyAsync(trace->logits, use_logits, (size_t)E * 4, hipMemcpyDeviceToDevice, s),
                                      error, capacity, "trace copy"))
@@ -792,13 +832,25 @@ __attribute__((visibility("default"))) int dih_moe_prefill(void *ctx, const dih_
                                                            const void *x, const void *logits, int logits_dtype,
                                                            void *residual, const dih_moe_trace *trace,
                                                            void *stream, char *error, int capacity) {
+    return dih_moe_prefill_norm(ctx, L, tokens, x, logits, logits_dtype, residual, nullptr, trace, stream, error,
+                                capacity);
+}
+
+__attribute__((visibility("default"))) int dih_moe_prefill_norm(void *ctx, const dih_moe_layer *L, int tokens,
+                                                                const void *x, const void *logits,
+                                                                int logits_dtype, void *residual,
+                                                                const dih_moe_merge *merge,
+                                                                const dih_moe_trace *trace, void *stream,
+                                                                char *error, int capacity) {
     Context *c = as_ctx(ctx);
     int E, H, I, Is;
+    MergeOut mo;
     if (!c || !x || !logits || !residual || tokens < 1 || tokens > (1 << 20) ||
         (logits_dtype != DIH_F32 && logits_dtype != DIH_BF16)) {
         set_error(error, capacity, "Invalid prefill MoE arguments");
         return -1;
     }
+    if (!merge_of(merge, residual, mo, error, capacity)) return -1;
     if (!check_layer(c, L, false, &E, &H, &I, &Is, error, capacity)) return -1;
     Matrix *gate = as_mat(L->gate), *up = as_mat(L->up), *down = as_mat(L->down);
     Matrix *sg = as_mat(L->shared_gate), *su = as_mat(L->shared_up), *sd = as_mat(L->shared_down);
@@ -835,8 +887,8 @@ __attribute__((visibility("default"))) int dih_moe_prefill(void *ctx, const dih_
     d.x = actb; d.in_mode = 0; d.y = route_out; d.y_bf16 = 0;
     if (!launch_qmm(d, s, error, capacity)) return -1;
     prof_mark(c, s, "prefill_down");
-    if (!launch_moe_merge(sr, static_cast<const uint16_t *>(x), tokens, H, route_out, probs,
-                          static_cast<uint16_t *>(residual), s, error, capacity))
+    if (!launch_moe_merge(sr, static_cast<const uint16_t *>(x), tokens, H, route_out, probs, residual, mo, s,
+                          error, capacity))
         return -1;
     prof_mark(c, s, "prefill_merge");
     if (trace) {

@@ -12,7 +12,7 @@
 //   K3 down + merge   : blocks of nine waves; waves 0..7 compute the selected experts'
 //                       down rows for the block's output rows, wave 8 the shared expert's;
 //                       the merge y = sigmoid(route)*shared + sum_slot p_slot*expert_slot
-//                       (slot order 0..7) and residual = bf16(residual + y) happen in LDS.
+//                       (slot order 0..7) and residual += y (f32 or bf16 storage) happen in LDS.
 //
 // Kernel boundaries are the only cross-block synchronization: on MI355X a device-scope
 // counter or flag shared by hundreds of blocks costs more than a launch. Every wave issues
@@ -236,7 +236,8 @@ struct DecodeParams {
     float *act;                                             // [8, I]
     uint32_t *ids; float *probs; uint32_t *status;          // published by K2
     const uint16_t *x;                                      // bf16 [H]
-    uint16_t *residual;                                     // bf16 [H]
+    void *residual;                                         // bf16 or f32 [H]
+    int residual_f32;
     float *route_out;                                       // optional [9, H]
     int E, H, I;
     int lpr_h, lpr_i;
@@ -459,7 +460,9 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
     float pr[8];
 #pragma unroll
     for (int s = 0; s < 8; s++) pr[s] = P.probs[s];
-    const uint32_t rbits = P.residual[h < P.H ? h : P.H - 1];
+    const int hc = h < P.H ? h : P.H - 1;
+    const uint32_t rbits = P.residual_f32 ? static_cast<const uint32_t *>(P.residual)[hc]
+                                          : (uint32_t) static_cast<const uint16_t *>(P.residual)[hc];
     const bool shared = wave == 8;
     // activations first (NV coalesced float4 per thread), then the expert id (a
     // wave-uniform scalar load, so waiting for it does not wait for the activations), then
@@ -509,7 +512,7 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
         float y = sh * sigmoidf_(route);
 #pragma unroll
         for (int s = 0; s < 8; s++) y += part[s][lane] * pr[s];
-        P.residual[h] = f32_to_bf16(bf16_to_f32(rbits) + y);
+        residual_store(P.residual, P.residual_f32, h, (P.residual_f32 ? __uint_as_float(rbits) : bf16_to_f32(rbits)) + y);
         if (P.route_out) {
 #pragma unroll
             for (int s = 0; s < 8; s++) P.route_out[(size_t)s * P.H + h] = part[s][lane];
@@ -553,7 +556,7 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
     P.dp = a.down->packed(); P.ds = a.down->scales(); P.db = a.down->biases();
     P.sdp = a.shared_down->packed(); P.sds = a.shared_down->scales(); P.sdb = a.shared_down->biases();
     P.act = a.act; P.ids = a.ids; P.probs = a.probs; P.status = a.status;
-    P.x = a.x; P.residual = a.residual; P.route_out = a.route_out;
+    P.x = a.x; P.residual = a.residual; P.residual_f32 = a.residual_f32; P.route_out = a.route_out;
     P.nchunks = (P.E + kChunkExperts - 1) / kChunkExperts;
     const int rows_per_block = kWaves * (64 / P.lpr_h);
     P.shared_blocks = (P.I + rows_per_block - 1) / rows_per_block;

@@ -30,6 +30,20 @@ DIH_DEV uint32_t pack_bf16x2(float lo, float hi) {
 }
 DIH_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
+// Residual storage: f32 (the reference's) or bf16 bit patterns.
+DIH_DEV float residual_load(const void *r, int f32, size_t i) {
+    return f32 ? static_cast<const float *>(r)[i] : bf16_to_f32(static_cast<const uint16_t *>(r)[i]);
+}
+DIH_DEV float residual_store(void *r, int f32, size_t i, float v) {  // returns the stored value
+    if (f32) {
+        static_cast<float *>(r)[i] = v;
+        return v;
+    }
+    const uint16_t b = f32_to_bf16(v);
+    static_cast<uint16_t *>(r)[i] = b;
+    return bf16_to_f32(b);
+}
+
 template <int BITS>
 struct Chunk {
     uint32_t w[BITS];  // 32 codes * BITS bits = BITS dwords

@@ -120,10 +120,26 @@ struct Top8Source {
 bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8,
                 hipStream_t s, char *error, int capacity);
 
+// Residual update and next-layer norm of the MoE steps (graph_merge_norm,
+// gpu_graph.mm:48-61; prefill_merge, gpu_prefill.mm:140-150): residual += y in f32 or bf16
+// storage; with norm_w, normed = r * rsqrt(mean(r^2) + eps) * norm_w of the stored r.
+struct MergeOut {
+    int residual_f32 = 0;
+    const float *norm_w = nullptr;
+    float eps = 0.f;
+    void *normed = nullptr;
+    int normed_f32 = 0;
+};
+
 bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t *ids,
                            const float *probs, const float *shared_out, const float *sroute,
-                           uint16_t *residual, float *route_out, hipStream_t s, char *error,
-                           int capacity);
+                           void *residual, int residual_f32, float *route_out, hipStream_t s,
+                           char *error, int capacity);
+
+// normed[t] = r[t] * rsqrt(mean(r[t]^2) + eps) * w, one block per token (the norm half of
+// graph_merge_norm / prefill_add_norm, gpu_graph.mm:40-61).
+bool launch_rmsnorm(const void *r, int r_f32, int tokens, int hidden, const float *w, float eps,
+                    void *out, int out_f32, hipStream_t s, char *error, int capacity);
 
 bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, uint32_t *ids,
                  float *probs, uint32_t *status, float *logits_copy, uint32_t *zero_word,
@@ -149,8 +165,8 @@ struct QmmArgs {
 bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity);
 
 bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens, int hidden,
-                      const float *route_out, const float *probs, uint16_t *residual,
-                      hipStream_t s, char *error, int capacity);
+                      const float *route_out, const float *probs, void *residual,
+                      const MergeOut &mo, hipStream_t s, char *error, int capacity);
 
 // Decode MoE step in three launches (decode.hip). Device buffers: logits [E], cand
 // [ceil(E/32)*8] float2, sact [I], sroute [1], act [8*I], ids [8], probs [8], status [1]
@@ -167,7 +183,8 @@ struct DecodeLaunch {
     float *probs = nullptr;
     uint32_t *status = nullptr;
     const uint16_t *x = nullptr;
-    uint16_t *residual = nullptr;
+    void *residual = nullptr;
+    int residual_f32 = 0;
     float *route_out = nullptr;
 };
 bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix *down, const Matrix *sg,

@@ -121,17 +121,19 @@ bool launch_build_groups(const uint32_t *ids, int tokens, int experts, int with_
 
 // ---------------------------------------------------------------------------- merge
 
-// One block per token (prefill_merge gpu_prefill.mm:140-150 without the next-layer
-// norm): gate = sigmoid(shared_route . x[t]); y = gate*out[T*8+t] + sum_{slot 0..7}
-// p*out[t*8+slot]; residual[t] = bf16(residual[t] + y).
+// One block per token (prefill_merge gpu_prefill.mm:140-150): gate = sigmoid(shared_route .
+// x[t]); y = gate*out[T*8+t] + sum_{slot 0..7} p*out[t*8+slot]; residual[t] += y (f32 or
+// bf16 storage); with norm_w, normed[t] = r * rsqrt(mean(r^2) + eps) * norm_w over the
+// stored r (each thread re-reads only the elements it wrote).
 template <int BITS>
 __global__ __launch_bounds__(256) void merge_kernel(const uint32_t *sr_packed,
                                                     const uint16_t *sr_scales,
                                                     const uint16_t *sr_biases,
                                                     const uint16_t *x, int tokens, int H,
                                                     const float *route_out, const float *probs,
-                                                    uint16_t *residual) {
+                                                    void *residual, MergeOut mo) {
     __shared__ float part[4];
+    __shared__ float sq[4];
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nchunk = H >> 5;
     float d = 0.f;
@@ -154,27 +156,71 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint32_t *sr_packed,
     for (int s = 0; s < 8; s++) p[s] = probs[(size_t)t * 8 + s];
     const float *sh = route_out + ((size_t)tokens * 8 + t) * H;
     const float *ro = route_out + (size_t)t * 8 * H;
+    float ss = 0.f;
     for (int c = tid; c < H; c += 256) {
         float y = sh[c] * gate;
 #pragma unroll
         for (int s = 0; s < 8; s++) y += ro[(size_t)s * H + c] * p[s];
         const size_t at = (size_t)t * H + c;
-        residual[at] = f32_to_bf16(bf16_to_f32(residual[at]) + y);
+        const float r = residual_store(residual, mo.residual_f32, at, residual_load(residual, mo.residual_f32, at) + y);
+        ss += r * r;
+    }
+    if (!mo.norm_w) return;  // uniform over the launch
+    ss = wave_sum(ss);
+    if (lane == 0) sq[wave] = ss;
+    __syncthreads();
+    const float scale = rsqrtf(((sq[0] + sq[1]) + (sq[2] + sq[3])) / (float)H + mo.eps);
+    for (int c = tid; c < H; c += 256) {
+        const size_t at = (size_t)t * H + c;
+        const float v = residual_load(residual, mo.residual_f32, at) * scale * mo.norm_w[c];
+        if (mo.normed_f32) static_cast<float *>(mo.normed)[at] = v;
+        else static_cast<uint16_t *>(mo.normed)[at] = f32_to_bf16(v);
     }
 }
 
 bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens, int hidden,
-                      const float *route_out, const float *probs, uint16_t *residual,
-                      hipStream_t s, char *error, int capacity) {
+                      const float *route_out, const float *probs, void *residual,
+                      const MergeOut &mo, hipStream_t s, char *error, int capacity) {
     if (shared_route->bits == 8)
         DIH_LAUNCH((merge_kernel<8>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
                            shared_route->scales(), shared_route->biases(), x, tokens, hidden, route_out,
-                           probs, residual);
+                           probs, residual, mo);
     else
         DIH_LAUNCH((merge_kernel<5>), dim3(tokens), dim3(256), 0, s, shared_route->packed(),
                            shared_route->scales(), shared_route->biases(), x, tokens, hidden, route_out,
-                           probs, residual);
+                           probs, residual, mo);
     return hip_ok(hipGetLastError(), error, capacity, "merge launch");
+}
+
+// ---------------------------------------------------------------------------- norm
+
+// One block per token: normed[t] = r[t] * rsqrt(sum(r[t]^2)/H + eps) * w (the norm of
+// graph_merge_norm / prefill_add_norm, gpu_graph.mm:40-61).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const void *r, int r_f32, int H, const float *w,
+                                                      float eps, void *out, int out_f32) {
+    __shared__ float sq[4];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f;
+    for (int c = tid; c < H; c += 256) {
+        const float v = residual_load(r, r_f32, (size_t)t * H + c);
+        ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) sq[wave] = ss;
+    __syncthreads();
+    const float scale = rsqrtf(((sq[0] + sq[1]) + (sq[2] + sq[3])) / (float)H + eps);
+    for (int c = tid; c < H; c += 256) {
+        const size_t at = (size_t)t * H + c;
+        const float v = residual_load(r, r_f32, at) * scale * w[c];
+        if (out_f32) static_cast<float *>(out)[at] = v;
+        else static_cast<uint16_t *>(out)[at] = f32_to_bf16(v);
+    }
+}
+
+bool launch_rmsnorm(const void *r, int r_f32, int tokens, int hidden, const float *w, float eps,
+                    void *out, int out_f32, hipStream_t s, char *error, int capacity) {
+    DIH_LAUNCH(rmsnorm_kernel, dim3(tokens), dim3(256), 0, s, r, r_f32, hidden, w, eps, out, out_f32);
+    return hip_ok(hipGetLastError(), error, capacity, "norm launch");
 }
 
 // --------------------------------------------------------------------------- argmax

@@ -253,7 +253,7 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
 // Decode expert down projection for the eight selected slots fused with the MoE merge
 // (quant_rows batched down + graph_merge_norm's weighted sum, gpu_graph.mm:48-61, and
 // Qwen36Model.cs:242-244): y = sigmoid(sroute)*shared_out[h] + sum_{slot 0..7}
-// p_slot * (down[e_slot][h] . act[slot]); residual[h] = bf16(residual[h] + y).
+// p_slot * (down[e_slot][h] . act[slot]); residual[h] += y (f32 or bf16 storage).
 // A block of eight waves owns ROWS output rows; wave w computes slot w for all of them
 // (its activation chunk is loaded once), the slot results meet in LDS and the first ROWS
 // threads merge them in slot order.
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(512) void moe_down_merge_kernel(
     const uint16_t *__restrict__ biases, int H, int I, const float *__restrict__ act,
     const uint32_t *__restrict__ ids, const float *__restrict__ probs,
     const float *__restrict__ shared_out, const float *__restrict__ sroute,
-    uint16_t *__restrict__ residual, float *__restrict__ route_out) {
+    void *__restrict__ residual, int residual_f32, float *__restrict__ route_out) {
     constexpr int GROUPS = 64 / LPR;                      // rows per pass of a wave
     constexpr int ROWS = GROUPS > 16 ? GROUPS : 16;       // output rows per block
     constexpr int PASSES = ROWS / GROUPS;
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(512) void moe_down_merge_kernel(
             float y = sh * sigmoidf_(sroute[0]);
 #pragma unroll
             for (int q = 0; q < 8; q++) y += part[q][r] * probs[q];
-            residual[h] = f32_to_bf16(bf16_to_f32(residual[h]) + y);
+            residual_store(residual, residual_f32, h, residual_load(residual, residual_f32, h) + y);
             if (route_out) {
 #pragma unroll
                 for (int q = 0; q < 8; q++) route_out[(size_t)q * H + h] = part[q][r];
@@ -322,8 +322,8 @@ __global__ __launch_bounds__(512) void moe_down_merge_kernel(
 
 bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t *ids,
                            const float *probs, const float *shared_out, const float *sroute,
-                           uint16_t *residual, float *route_out, hipStream_t s, char *error,
-                           int capacity) {
+                           void *residual, int residual_f32, float *route_out, hipStream_t s,
+                           char *error, int capacity) {
     const int H = down->rows, I = down->columns;
     const int nchunk = I / 32;
     if (nchunk > 64) {
@@ -337,7 +337,7 @@ bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t 
     if (down->bits == B && lpr == L) {                                                               \
         DIH_LAUNCH((moe_down_merge_kernel<B, L>), dim3(blocks), dim3(512), 0, s, down->packed(),     \
                    down->scales(), down->biases(), H, I, act, ids, probs, shared_out, sroute,        \
-                   residual, route_out);                                                             \
+                   residual, residual_f32, route_out);                                               \
         return hip_ok(hipGetLastError(), error, capacity, "down/merge launch");                      \
     }
     DIH_DM_CASE(8, 2) DIH_DM_CASE(8, 4) DIH_DM_CASE(8, 8) DIH_DM_CASE(8, 16) DIH_DM_CASE(8, 32) DIH_DM_CASE(8, 64)

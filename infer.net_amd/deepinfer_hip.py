@@ -69,6 +69,12 @@ class MoeTrace(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ("logits", "ids", "probs", "expert_out", "status")]
 
 
+class MoeMerge(ctypes.Structure):
+    """dih_moe_merge: residual storage and the fused next-layer RMSNorm."""
+    _fields_ = [("residual_f32", ctypes.c_int), ("norm_weight", ctypes.c_void_p), ("epsilon", ctypes.c_float),
+                ("normed", ctypes.c_void_p), ("normed_f32", ctypes.c_int)]
+
+
 EXPORTS = [
     "dih_quant_create", "dih_quant_create_configured", "dih_quant_destroy",
     "dih_quant_residency_bytes", "dih_quant_residency_prepare", "dih_quant_matrix_create",
@@ -76,7 +82,8 @@ EXPORTS = [
     "dih_quant_matrix_commit", "dih_quant_matrix_device", "dih_quant_matrix_shape",
     "dih_quant_batch", "dih_quant_matvec", "dih_quant_experts", "dih_quant_embedding",
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
-    "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_dense", "dih_set_profiling",
+    "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm",
+    "dih_moe_prefill_norm", "dih_dense", "dih_set_profiling",
     "dih_profile_read", "dih_version",
     "dih_safetensors_open", "dih_safetensors_close", "dih_safetensors_count",
     "dih_safetensors_info", "dih_safetensors_get", "dih_safetensors_read",
@@ -125,6 +132,8 @@ def load():
         "dih_dequant_bf16": ([P, P, I, P, P, E, I], I),
         "dih_moe_decode": ([P, P, P, P, P, P, P, E, I], I),
         "dih_moe_prefill": ([P, P, I, P, P, I, P, P, P, E, I], I),
+        "dih_moe_decode_norm": ([P, P, P, P, P, P, P, P, E, I], I),
+        "dih_moe_prefill_norm": ([P, P, I, P, P, I, P, P, P, P, E, I], I),
         "dih_dense": ([P, P, I, P, P, I, P, E, I], I),
         "dih_set_profiling": ([P, I], I),
         "dih_profile_read": ([P, P, P, P, I], I),
@@ -509,20 +518,26 @@ def make_trace(logits=None, ids=None, probs=None, expert_out=None, status=None) 
     return MoeTrace(_dp(logits), _dp(ids), _dp(probs), _dp(expert_out), _dp(status))
 
 
+def make_merge(residual_f32=False, norm_weight=None, epsilon=1e-6, normed=None, normed_f32=True) -> MoeMerge:
+    return MoeMerge(1 if residual_f32 else 0, _dp(norm_weight), epsilon, _dp(normed), 1 if normed_f32 else 0)
+
+
 def moe_decode(dev, layer: MoeLayer, x, residual, logits=None, trace: Optional[MoeTrace] = None,
-               stream=None) -> None:
+               stream=None, merge: Optional[MoeMerge] = None) -> None:
     err = _errbuf()
-    _check(dev._lib.dih_moe_decode(_ctx(dev), ctypes.byref(layer), _dp(x), _dp(logits), _dp(residual),
-                                   None if trace is None else ctypes.byref(trace), _stream(stream), err, _ERR),
+    _check(dev._lib.dih_moe_decode_norm(_ctx(dev), ctypes.byref(layer), _dp(x), _dp(logits), _dp(residual),
+                                        None if merge is None else ctypes.byref(merge),
+                                        None if trace is None else ctypes.byref(trace), _stream(stream), err, _ERR),
            err, ArgumentError)
 
 
 def moe_prefill(dev, layer: MoeLayer, tokens, x, logits, residual, logits_dtype=BF16,
-                trace: Optional[MoeTrace] = None, stream=None) -> None:
+                trace: Optional[MoeTrace] = None, stream=None, merge: Optional[MoeMerge] = None) -> None:
     err = _errbuf()
-    _check(dev._lib.dih_moe_prefill(_ctx(dev), ctypes.byref(layer), tokens, _dp(x), _dp(logits), logits_dtype,
-                                    _dp(residual), None if trace is None else ctypes.byref(trace),
-                                    _stream(stream), err, _ERR), err, ArgumentError)
+    _check(dev._lib.dih_moe_prefill_norm(_ctx(dev), ctypes.byref(layer), tokens, _dp(x), _dp(logits),
+                                         logits_dtype, _dp(residual), None if merge is None else ctypes.byref(merge),
+                                         None if trace is None else ctypes.byref(trace), _stream(stream), err,
+                                         _ERR), err, ArgumentError)
 
 
 def dense(dev, m, tokens, x, y, y_dtype=F32, stream=None) -> None:

@@ -258,6 +258,24 @@ def moe_f64(layer: MoeLayer, x: np.ndarray, ids: np.ndarray, probs: np.ndarray,
     return (y, ro) if route_out else y
 
 
+def merge_norm_f64(residual, y, weight=None, epsilon=1e-6, residual_bf16=False):
+    """MoE merge into the residual and the next layer's RMSNorm (graph_merge_norm,
+    gpu_graph.mm:48-61; prefill_merge, gpu_prefill.mm:140-150), rows = tokens:
+    r = residual + y, stored in f32 (the reference) or as bf16 (RNE); normed =
+    r * (mean(r^2) + eps)^-1/2 * weight over the stored r. Returns (stored r, normed) in
+    float64 (normed None without weight)."""
+    r = np.asarray(residual, dtype=np.float64) + np.asarray(y, dtype=np.float64)
+    r = np.atleast_2d(r)
+    if residual_bf16:
+        stored = bf16_bits_to_f32(f32_to_bf16_bits(r.astype(np.float32))).astype(np.float64)
+    else:
+        stored = r.astype(np.float32).astype(np.float64)
+    if weight is None:
+        return stored, None
+    inv = 1.0 / np.sqrt(np.mean(stored * stored, axis=1, keepdims=True) + float(epsilon))
+    return stored, stored * inv * np.asarray(weight, dtype=np.float64)[None, :]
+
+
 def cpu_qmv(m: QMatrix, x, experts=None, batched=False, threads=1) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     count = 1 if experts is None else len(experts)

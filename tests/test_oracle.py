@@ -278,3 +278,27 @@ def test_cpu_moe_token_matches_fp64():
     ids, probs = orc.top8(logits)
     want = orc.moe_f64(L, x[None, :], ids[None, :], probs[None, :], bf16_operands=False)[0]
     assert orc.rel_err(y, want) < 1e-4
+
+
+def test_merge_norm_closed_forms():
+    """merge_norm_f64 pinned by closed forms of RMSNorm: a constant row c gives
+    c / sqrt(c^2 + eps) * w; a row scaled by k gives k r / sqrt(k^2 mean(r^2) + eps) * w; bf16
+    storage rounds r before the norm; eps enters once, under the square root."""
+    w = np.linspace(0.5, 2.0, 64)
+    for c, eps in ((3.0, 1e-6), (-0.25, 1e-2), (1e-3, 1e-6)):
+        stored, normed = orc.merge_norm_f64(np.full((1, 64), c - 1.0), np.ones((1, 64)), w, eps)
+        assert np.allclose(stored, c, rtol=1e-6) and np.all(stored == stored[0, 0])
+        cs = stored[0, 0]                      # c after the f32 storage rounding
+        assert np.allclose(normed[0], cs / np.sqrt(cs * cs + eps) * w, rtol=1e-12)
+    rng = np.random.default_rng(1)
+    r = rng.normal(size=(3, 64)).astype(np.float32).astype(np.float64)
+    for k in (2.0, 0.5, 1024.0):
+        _, a = orc.merge_norm_f64(k * r, np.zeros_like(r), w, 1e-6)
+        ms = np.mean(r * r, axis=1, keepdims=True)
+        assert np.allclose(a, k * r / np.sqrt(k * k * ms + 1e-6) * w, rtol=1e-12)
+    # bf16 storage: 1 + 2^-9 rounds to 1 (tie to even), 1 + 3*2^-9 to 1 + 2^-7
+    s, _ = orc.merge_norm_f64(np.array([[1.0, 1.0]]), np.array([[2.0 ** -9, 3 * 2.0 ** -9]]), residual_bf16=True)
+    assert s.tolist() == [[1.0, 1.0 + 2.0 ** -7]]
+    # f32 storage: the sum is rounded to f32 before the norm
+    s, _ = orc.merge_norm_f64(np.array([[1.0]]), np.array([[2.0 ** -30]]))
+    assert s.tolist() == [[1.0]]

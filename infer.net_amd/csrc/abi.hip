@@ -738,7 +738,7 @@ __attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const 
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);
     if (decode_fast_path_ok(router, gate, down, sg, sd, sr)) {
-        float2 *cand = static_cast<float2 *>(scratch(c, S_CAND, 64 * sizeof(float2), error, capacity));
+        float2 *cand = static_cast<float2 *>(scratch(c, S_CAND, 128 * sizeof(float2), error, capacity));
         if (!cand) return -1;
         DecodeLaunch a;
         a.router = router; a.gate = gate; a.up = up; a.down = down;

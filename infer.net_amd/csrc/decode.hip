@@ -2,13 +2,13 @@
 // graph_top8 gpu_graph.mm:134-146 and graph_merge_norm gpu_graph.mm:48-61; host form
 // Qwen36Model.cs:218-245):
 //
-//   K1 router/shared  : router logits in 32-expert chunks; each chunk block ranks its 32
-//                       logits in LDS and writes its top-8 as candidates (value, id).
-//                       The same launch computes the shared expert's gate/up SwiGLU and the
-//                       shared-expert sigmoid gate row.
-//   K2 experts gate/up: every wave merges the <= 64 candidates by rank (the top-8 of the
+//   K1 router/shared  : four-wave blocks spread over many CUs. Router logits in 16-expert
+//                       chunks; each chunk block ranks its 16 logits in LDS and writes its
+//                       top-8 as candidates (value, id). The same launch computes the
+//                       shared expert's gate/up SwiGLU and the shared-expert sigmoid gate row.
+//   K2 experts gate/up: every block merges the <= 128 candidates by rank (the top-8 of the
 //                       union of per-chunk top-8s is the global top-8, ties to the lowest
-//                       id) and streams four gated rows of its slot's expert.
+//                       id) and streams one gated row group per wave of its slot's expert.
 //   K3 down + merge   : blocks of nine waves; waves 0..7 compute the selected experts'
 //                       down rows for the block's output rows, wave 8 the shared expert's;
 //                       the merge y = sigmoid(route)*shared + sum_slot p_slot*expert_slot
@@ -25,9 +25,11 @@ namespace dih {
 
 namespace {
 
-constexpr int kChunkExperts = 32;  // experts per router block
-constexpr int kWaves = 16;         // waves per K1/K2 block
-constexpr int kRouterGroups = 2;   // K1 router: row groups per wave (32 rows per block)
+constexpr int kChunkExperts = 16;  // experts per router block (a block's top-8 are candidates)
+constexpr int kK1Waves = 4;        // waves per K1 block: the launch spreads over many CUs
+constexpr int kWaves = 16;         // waves per K2 block
+constexpr int kRouterGroups = 4;   // K1 router: row groups per wave (16 rows per block)
+constexpr int kMaxCand = 128;      // candidates: 8 per chunk, at most 256 experts
 constexpr int kDownGroups = 2;     // K3: row groups per wave
 
 // One lane's share of NG row groups of one matrix.
@@ -250,7 +252,7 @@ struct DecodeParams {
 // ------------------------------------------------------------------------------- K1
 
 template <int BITS>
-__global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
+__global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
     __shared__ __align__(16) float xl[2048];
     __shared__ float xsl[64];
     __shared__ __align__(16) uint32_t xh[1024];
@@ -260,7 +262,7 @@ __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
     const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     if (b < P.nchunks) {
-        // router rows b*32 + wave*2*rpw + q*rpw + g (8-bit); rows past the chunk are masked
+        // router rows b*16 + wave*4*rpw + q*rpw + g (8-bit); rows past the chunk are masked
         const int wrow = wave * kRouterGroups * L.rpw;
         const int base = b * kChunkExperts + wrow;
         const int n = min(kChunkExperts, P.E - b * kChunkExperts);
@@ -297,18 +299,19 @@ __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
         }
         __syncthreads();
         if (wave == 0) {
-            // rank of each of the chunk's logits: lane c and lane c + 32 each count the
-            // keys of one half of the chunk that order before candidate c (broadcast LDS
+            // rank of each of the chunk's logits: lanes c, c+16, c+32, c+48 each count the
+            // keys of one quarter of the chunk that order before candidate c (broadcast LDS
             // reads, one 64-bit compare per key); the eight first become candidates
-            const int c = lane & 31, half = lane >> 5;
+            const int c = lane & 15, quarter = lane >> 4;
             const unsigned long long me = lkey[c];
             int rank = 0;
 #pragma unroll
-            for (int k = 0; k < kChunkExperts / 2; k += 2) {
-                const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&lkey[half * (kChunkExperts / 2) + k]);
+            for (int k = 0; k < kChunkExperts / 4; k += 2) {
+                const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&lkey[quarter * (kChunkExperts / 4) + k]);
                 rank += q.x > me ? 1 : 0;
                 rank += q.y > me ? 1 : 0;
             }
+            rank += __shfl_xor(rank, 16, 64);
             rank += __shfl_xor(rank, 32, 64);
             const bool mine = lane < n;
             const float v = lg[c];
@@ -325,7 +328,7 @@ __global__ __launch_bounds__(1024) void decode_router_kernel(DecodeParams P) {
     const int sb = b - P.nchunks;
     if (sb < P.shared_blocks) {
         // shared expert gate/up SwiGLU: one row group (rpw rows) per wave
-        const int base = (sb * kWaves + wave) * L.rpw;
+        const int base = (sb * kK1Waves + wave) * L.rpw;
         const uint4 xv = stage_x_load(P.x, P.H);
         Rows<BITS, 1> G, U;
         rows_load<BITS, 1>(G, P.sgp, P.sgs, P.sgb, 0, P.I, base, L.rpw, L.g, L.jc, P.H);
@@ -370,20 +373,20 @@ __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
     __shared__ float xsl[BITS == 8 ? 1 : 64];
     __shared__ __align__(16) uint32_t xh[BITS == 8 ? 1024 : 1];
     __shared__ float xhs[BITS == 8 ? 64 : 1], xhm[BITS == 8 ? 64 : 1];
-    __shared__ __align__(16) float2 cl[64];
-    __shared__ int rk[64];
+    __shared__ __align__(16) float2 cl[kMaxCand];
+    __shared__ int rk[kMaxCand];
     __shared__ uint32_t chosen[8];
     __shared__ float chosen_v[8];
     __shared__ int any_bad;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int t = threadIdx.x, wave = t >> 6;
     const int slot = blockIdx.x / P.gate_blocks;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     const int base = ((blockIdx.x - slot * P.gate_blocks) * kWaves + wave) * L.rpw;
     // candidates -> rank -> this slot's expert, ranked once per block: thread t compares
-    // candidate t%64 with the four candidates of sixteenth t/64 (slots past nc hold
+    // candidate t%128 with the sixteen candidates of eighth t/128 (slots past nc hold
     // (-inf, 0xffffffff), which no candidate ranks behind)
     const int nc = P.nchunks * 8;
-    if (t < 64) {
+    if (t < kMaxCand) {
         cl[t] = t < nc ? P.cand[t] : make_float2(-INFINITY, __uint_as_float(0xffffffffu));
         rk[t] = 0;
         if (t == 0) any_bad = 0;
@@ -392,16 +395,18 @@ __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
     else stage_x_store(stage_x_load(P.x, P.H), P.H, xl, xsl);
     __syncthreads();
     {
-        const float2 me = cl[lane];
+        const int c = t & (kMaxCand - 1), g = t / kMaxCand;
+        const float2 me = cl[c];
         const uint32_t mid = __float_as_uint(me.y);
-        const float4 q0 = *reinterpret_cast<const float4 *>(&cl[wave * 4]);
-        const float4 q1 = *reinterpret_cast<const float4 *>(&cl[wave * 4 + 2]);
-        int r = before(q0.x, __float_as_uint(q0.y), me.x, mid) ? 1 : 0;
-        r += before(q0.z, __float_as_uint(q0.w), me.x, mid) ? 1 : 0;
-        r += before(q1.x, __float_as_uint(q1.y), me.x, mid) ? 1 : 0;
-        r += before(q1.z, __float_as_uint(q1.w), me.x, mid) ? 1 : 0;
-        if (r) atomicAdd(&rk[lane], r);
-        if (wave == 0 && lane < nc && mid == 0xfffffffeu) any_bad = 1;
+        int r = 0;
+#pragma unroll
+        for (int k = 0; k < kMaxCand / 8; k += 2) {
+            const float4 q = *reinterpret_cast<const float4 *>(&cl[g * (kMaxCand / 8) + k]);
+            r += before(q.x, __float_as_uint(q.y), me.x, mid) ? 1 : 0;
+            r += before(q.z, __float_as_uint(q.w), me.x, mid) ? 1 : 0;
+        }
+        if (r) atomicAdd(&rk[c], r);
+        if (g == 0 && c < nc && mid == 0xfffffffeu) any_bad = 1;
     }
     __syncthreads();
     if (t < nc && rk[t] < 8) {
@@ -558,9 +563,9 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
     P.act = a.act; P.ids = a.ids; P.probs = a.probs; P.status = a.status;
     P.x = a.x; P.residual = a.residual; P.residual_f32 = a.residual_f32; P.route_out = a.route_out;
     P.nchunks = (P.E + kChunkExperts - 1) / kChunkExperts;
-    const int rows_per_block = kWaves * (64 / P.lpr_h);
-    P.shared_blocks = (P.I + rows_per_block - 1) / rows_per_block;
-    P.gate_blocks = P.shared_blocks;
+    const int rpw = 64 / P.lpr_h;
+    P.shared_blocks = (P.I + kK1Waves * rpw - 1) / (kK1Waves * rpw);
+    P.gate_blocks = (P.I + kWaves * rpw - 1) / (kWaves * rpw);
     P.down_rows = std::min(64, kDownGroups * (64 / P.lpr_i));
     const int k1 = P.nchunks + P.shared_blocks + 1;
     const int k2 = 8 * P.gate_blocks;
@@ -568,7 +573,7 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
     const size_t k3_lds = (size_t)9 * P.I * 4 + (size_t)9 * (P.I / 32) * 4;
     if (gate->bits == 8) {
         prof_stage("decode_router_shared");
-        DIH_LAUNCH(decode_router_kernel<8>, dim3(k1), dim3(1024), 0, s, P);
+        DIH_LAUNCH(decode_router_kernel<8>, dim3(k1), dim3(256), 0, s, P);
         prof_stage("decode_experts_gate_up");
         DIH_LAUNCH(decode_experts_kernel<8>, dim3(k2), dim3(1024), 0, s, P);
         prof_stage("decode_down_merge");
@@ -580,7 +585,7 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
         else DIH_LAUNCH((decode_down_kernel<8, 4>), dim3(k3), dim3(576), k3_lds, s, P);
     } else {
         prof_stage("decode_router_shared");
-        DIH_LAUNCH(decode_router_kernel<5>, dim3(k1), dim3(1024), 0, s, P);
+        DIH_LAUNCH(decode_router_kernel<5>, dim3(k1), dim3(256), 0, s, P);
         prof_stage("decode_experts_gate_up");
         DIH_LAUNCH(decode_experts_kernel<5>, dim3(k2), dim3(1024), 0, s, P);
         prof_stage("decode_down_merge");

@@ -27,7 +27,7 @@ namespace {
 
 constexpr int kChunkExperts = 16;  // experts per router block (a block's top-8 are candidates)
 constexpr int kK1Waves = 4;        // waves per K1 block: the launch spreads over many CUs
-constexpr int kWaves = 16;         // waves per K2 block
+constexpr int kWaves = 16;         // waves per K2 block (at least 2: 128 candidate threads)
 constexpr int kRouterGroups = 4;   // K1 router: row groups per wave (16 rows per block)
 constexpr int kMaxCand = 128;      // candidates: 8 per chunk, at most 256 experts
 constexpr int kDownGroups = 2;     // K3: row groups per wave
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
 // ------------------------------------------------------------------------------- K2
 
 template <int BITS>
-__global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
+__global__ __launch_bounds__(kWaves * 64) void decode_experts_kernel(DecodeParams P) {
     __shared__ __align__(16) float xl[BITS == 8 ? 1 : 2048];
     __shared__ float xsl[BITS == 8 ? 1 : 64];
     __shared__ __align__(16) uint32_t xh[BITS == 8 ? 1024 : 1];
@@ -383,8 +383,8 @@ __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     const int base = ((blockIdx.x - slot * P.gate_blocks) * kWaves + wave) * L.rpw;
     // candidates -> rank -> this slot's expert, ranked once per block: thread t compares
-    // candidate t%128 with the sixteen candidates of eighth t/128 (slots past nc hold
-    // (-inf, 0xffffffff), which no candidate ranks behind)
+    // candidate t%128 with the candidates of part t/128 of kWaves/2 parts (slots past nc
+    // hold (-inf, 0xffffffff), which no candidate ranks behind)
     const int nc = P.nchunks * 8;
     if (t < kMaxCand) {
         cl[t] = t < nc ? P.cand[t] : make_float2(-INFINITY, __uint_as_float(0xffffffffu));
@@ -399,9 +399,10 @@ __global__ __launch_bounds__(1024) void decode_experts_kernel(DecodeParams P) {
         const float2 me = cl[c];
         const uint32_t mid = __float_as_uint(me.y);
         int r = 0;
+        constexpr int kPart = kMaxCand / (kWaves / 2);
 #pragma unroll
-        for (int k = 0; k < kMaxCand / 8; k += 2) {
-            const float4 q = *reinterpret_cast<const float4 *>(&cl[g * (kMaxCand / 8) + k]);
+        for (int k = 0; k < kPart; k += 2) {
+            const float4 q = *reinterpret_cast<const float4 *>(&cl[g * kPart + k]);
             r += before(q.x, __float_as_uint(q.y), me.x, mid) ? 1 : 0;
             r += before(q.z, __float_as_uint(q.w), me.x, mid) ? 1 : 0;
         }
@@ -575,7 +576,7 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
         prof_stage("decode_router_shared");
         DIH_LAUNCH(decode_router_kernel<8>, dim3(k1), dim3(256), 0, s, P);
         prof_stage("decode_experts_gate_up");
-        DIH_LAUNCH(decode_experts_kernel<8>, dim3(k2), dim3(1024), 0, s, P);
+        DIH_LAUNCH(decode_experts_kernel<8>, dim3(k2), dim3(kWaves * 64), 0, s, P);
         prof_stage("decode_down_merge");
         // float4 activation loads per K3 thread: 9 rows of I floats over 576 threads
         // (I <= 1024: at most four; the staged rows then take at most 37 KB of LDS)
@@ -587,7 +588,7 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
         prof_stage("decode_router_shared");
         DIH_LAUNCH(decode_router_kernel<5>, dim3(k1), dim3(256), 0, s, P);
         prof_stage("decode_experts_gate_up");
-        DIH_LAUNCH(decode_experts_kernel<5>, dim3(k2), dim3(1024), 0, s, P);
+        DIH_LAUNCH(decode_experts_kernel<5>, dim3(k2), dim3(kWaves * 64), 0, s, P);
         prof_stage("decode_down_merge");
         const int nv = (9 * (P.I / 4) + 575) / 576;
         if (nv <= 1) DIH_LAUNCH((decode_down_kernel<5, 1>), dim3(k3), dim3(576), k3_lds, s, P);

@@ -357,6 +357,9 @@ DIH_DEV void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
+// s_waitcnt lgkmcnt(0) leaving the other counters alone
+DIH_DEV void wait_lgkm0() { __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14)); }
+
 // Workgroup barrier without a memory fence: __syncthreads() would also wait for every
 // outstanding copy (the fence counts LDS copies as pending stores). Callers first wait
 // for their own copies of the step with wait_vm; the "memory" clobber keeps the compiler
@@ -365,34 +368,46 @@ DIH_DEV void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
 
 // Blocks per CU the streaming kernel is built for: two for the narrow route tiles (32 rows
 // of accumulators per matrix) when four stages fit in half the LDS; the VGPR budget is then
-// 256 per lane, accumulators included.
-template <int BITS, bool GATED, int NT>
+// 256 per lane, accumulators included. The split gated form (eight waves) runs one block.
+template <int BITS, bool GATED, int NT, bool SPLIT>
 constexpr int qmm_lds_occupancy() {
-    return (GATED ? 2 : 1) * NT <= 2 &&
+    return !SPLIT && (GATED ? 2 : 1) * NT <= 2 &&
                    4 * ((GATED ? 2 : 1) * 128 * (64 * BITS / 8) + 32 * NT * 128) <= 80 * 1024
                ? 2 : 1;
 }
 
-template <int BITS, bool GATED, int NT, int S>
-__global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void qmm_lds_kernel(QmmParams P) {
+// SPLIT (gated only): eight waves, waves 0-3 the gate matrix and 4-7 the up matrix of the
+// same four 32-row slabs, so that two waves share each SIMD and one's dequant overlaps the
+// other's MFMAs and waits; the SwiGLU epilogue meets the two halves in LDS.
+template <int BITS, bool GATED, int NT, int S, bool SPLIT>
+__global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
+    static_assert(!SPLIT || GATED, "only the gated kernel splits its matrices over waves");
+    constexpr int NW = SPLIT ? 8 : 4;        // waves per block
     constexpr int BN = 32 * NT;
     constexpr int AB = 64 * BITS / 8;        // bytes of one row's codes per K step
     constexpr int A_ST = 128 * AB;           // one matrix, one stage
     constexpr int NMAT = GATED ? 2 : 1;
+    constexpr int WMAT = SPLIT ? 1 : NMAT;   // matrices one wave dequantizes
     constexpr int B_ST = BN * 128;
     constexpr int ST = NMAT * A_ST + B_ST;   // bytes per stage
     constexpr int AQ = BITS == 8 ? 2 : 5;    // direct copies per wave per matrix per step
-    constexpr int LPS = NMAT * AQ + NT;      // copies per thread per step
+    constexpr int NBW = 4 * NT / NW;         // activation copies (8 routes each) per wave
+    static_assert(NBW >= 1 && NBW * NW == 4 * NT, "activation pieces split evenly over the waves");
+    constexpr int LPS = WMAT * AQ + NBW;     // copies per thread per step
     static_assert(S == 4, "the stage of step s is s % 4, static within the eight-step unroll");
     // one array per stage: with the stage known at compile time the compiler can tell that an
     // operand read does not alias the copies in flight to the other stages. Nothing else
-    // lives in LDS, so that two blocks fit on a CU when the stages take half of it.
+    // lives in LDS (the split form adds the SwiGLU exchange), so that two blocks fit on a
+    // CU when the stages take half of it.
     __shared__ __align__(16) unsigned char st0[ST], st1[ST], st2[ST], st3[ST];
+    __shared__ __align__(16) float xch[SPLIT ? 4 * NT * 16 * 64 : 1];
     auto stage_base = [&](int stage) -> unsigned char * {
         return stage == 0 ? st0 : stage == 1 ? st1 : stage == 2 ? st2 : st3;
     };
 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int slab = wave & 3;                // 32-row slab of the 128-row tile
+    const int mw = SPLIT ? wave >> 2 : 0;     // split: the matrix this wave computes
     // ---- work item (every wave derives it): physical block b runs logical item
     // L = (b % 8) * (grid / 8) + b / 8; L = chunk * rt_groups + row-tile group, a group
     // being up to rtb consecutive row tiles
@@ -443,11 +458,11 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
     for (int q = 0; q < AQ; q++) {
         if constexpr (BITS == 8) {
             const int rl = 16 * q + (lane >> 2), sl = lane & 3;
-            crow[q] = wave * 32 + rl;
+            crow[q] = slab * 32 + rl;
             coff[q] = 16 * (sl ^ ((rl >> 2) & 3));
         } else {
             const int i = 64 * q + lane, rl = i / 10;
-            crow[q] = wave * 32 + rl;
+            crow[q] = slab * 32 + rl;
             coff[q] = 4 * (i - rl * 10);
         }
     }
@@ -455,20 +470,20 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
     const int r = lane & 31, h = lane >> 5;
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     auto win_load = [&](u32x4 (&sw)[2][2], int ti, int w) {
-        const size_t mrow = row_index(rt0 + ti, wave * 32 + r);
+        const size_t mrow = row_index(rt0 + ti, slab * 32 + r);
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-            sw[m][0] = *reinterpret_cast<const u32x4 *>(psc[m] + mrow * G + 8 * w);
-            sw[m][1] = *reinterpret_cast<const u32x4 *>(pbi[m] + mrow * G + 8 * w);
+        for (int m = 0; m < WMAT; m++) {
+            sw[m][0] = *reinterpret_cast<const u32x4 *>(psc[m + mw] + mrow * G + 8 * w);
+            sw[m][1] = *reinterpret_cast<const u32x4 *>(pbi[m + mw] + mrow * G + 8 * w);
         }
     };
 
     // ---- routes -> input row offsets of this lane's activation copies
     const int T8 = P.tokens * 8;
-    const uint16_t *bsrc[NT];
+    const uint16_t *bsrc[NBW];
 #pragma unroll
-    for (int i = 0; i < NT; i++) {
-        const int n = (4 * i + wave) * 8 + (lane >> 3), sl = lane & 7;
+    for (int i = 0; i < NBW; i++) {
+        const int n = (NW * i + wave) * 8 + (lane >> 3), sl = lane & 7;
         const int route = route_at(n);
         const int in_row = P.in_mode == 1 ? (route < T8 ? (route >> 3) : route - T8) : route;
         bsrc[i] = P.x + (size_t)in_row * C + 8 * (sl ^ ((n >> 1) & 7));
@@ -484,18 +499,19 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
         const int ti = step / G, kg = step - ti * G;
         unsigned char *base = stage_base(stage);
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
+        for (int mm = 0; mm < WMAT; mm++) {
+            const int m = mm + mw;
 #pragma unroll
             for (int q = 0; q < AQ; q++) {
                 const char *src = pw[m] + row_index(rt0 + ti, crow[q]) * row_bytes + (size_t)kg * AB + coff[q];
                 if constexpr (BITS == 8)
-                    to_lds<16>(src, base + m * A_ST + (wave * 32 + 16 * q) * 64);
+                    to_lds<16>(src, base + m * A_ST + (slab * 32 + 16 * q) * 64);
                 else
-                    to_lds<4>(src, base + m * A_ST + wave * 32 * 40 + q * 256);
+                    to_lds<4>(src, base + m * A_ST + slab * 32 * 40 + q * 256);
             }
         }
 #pragma unroll
-        for (int i = 0; i < NT; i++) to_lds<16>(bsrc[i] + 64 * kg, base + NMAT * A_ST + (4 * i + wave) * 8 * 128);
+        for (int i = 0; i < NBW; i++) to_lds<16>(bsrc[i] + 64 * kg, base + NMAT * A_ST + (NW * i + wave) * 8 * 128);
     };
 
 #pragma unroll
@@ -503,14 +519,14 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
     u32x4 win[2][2], win_next[2][2];
     win_load(win, 0, 0);
 
-    dih_f32x16 acc0[NT], acc1[GATED ? NT : 1];
+    dih_f32x16 acc0[NT], acc1[GATED && !SPLIT ? NT : 1];
     auto zero_acc = [&]() {
 #pragma unroll
         for (int i = 0; i < NT; i++) {
 #pragma unroll
             for (int k = 0; k < 16; k++) acc0[i][k] = 0.f;
         }
-        if constexpr (GATED) {
+        if constexpr (GATED && !SPLIT) {
 #pragma unroll
             for (int i = 0; i < NT; i++) {
 #pragma unroll
@@ -535,17 +551,17 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
                 // this step's weights -> bf16 A operands
                 dih_bf16x8 a[2][4];
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) {
+                for (int m = 0; m < WMAT; m++) {
                     Chunk<BITS> c;
                     if constexpr (BITS == 8) {
                         const int sw = (r >> 2) & 3;
-                        const unsigned char *ra = base + m * A_ST + (wave * 32 + r) * 64;
+                        const unsigned char *ra = base + (m + mw) * A_ST + (slab * 32 + r) * 64;
                         const u32x4 v0 = *reinterpret_cast<const u32x4 *>(ra + 16 * ((2 * h) ^ sw));
                         const u32x4 v1 = *reinterpret_cast<const u32x4 *>(ra + 16 * ((2 * h + 1) ^ sw));
                         c.w[0] = v0.x; c.w[1] = v0.y; c.w[2] = v0.z; c.w[3] = v0.w;
                         c.w[4] = v1.x; c.w[5] = v1.y; c.w[6] = v1.z; c.w[7] = v1.w;
                     } else {
-                        const uint32_t *ra = reinterpret_cast<const uint32_t *>(base + m * A_ST) + (wave * 32 + r) * 10 + 5 * h;
+                        const uint32_t *ra = reinterpret_cast<const uint32_t *>(base + (m + mw) * A_ST) + (slab * 32 + r) * 10 + 5 * h;
 #pragma unroll
                         for (int k = 0; k < 5; k++) c.w[k] = ra[k];
                     }
@@ -566,24 +582,37 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
 #pragma unroll
                     for (int i = 0; i < NT; i++) {
                         acc0[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][j], bx[i], acc0[i], 0, 0, 0);
-                        if constexpr (GATED)
+                        if constexpr (GATED && !SPLIT)
                             acc1[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][j], bx[i], acc1[i], 0, 0, 0);
                     }
                 }
             }
             if (more) {
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) { win[m][0] = win_next[m][0]; win[m][1] = win_next[m][1]; }
+                for (int m = 0; m < WMAT; m++) { win[m][0] = win_next[m][0]; win[m][1] = win_next[m][1]; }
             }
         }
 
         // ---- epilogue of row tile rt0 + ti: lane holds route n = 32i + r, rows
-        // 8*(k/4) + 4h + (k%4) of the wave's 32
-        const int row_base = (rt0 + ti) * 128 + wave * 32;
+        // 8*(k/4) + 4h + (k%4) of the slab's 32. Split: the gate waves hand silu(g) to the up
+        // waves of the same slab through LDS (identical lane layouts); the up waves store.
+        if constexpr (SPLIT) {
+            float *xw = xch + slab * NT * 16 * 64 + lane;
+            if (mw == 0) {
+#pragma unroll
+                for (int i = 0; i < NT; i++) {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) xw[(i * 16 + k) * 64] = siluf_(acc0[i][k]);
+                }
+            }
+            wait_lgkm0();
+            barrier_no_fence();
+        }
+        const int row_base = (rt0 + ti) * 128 + slab * 32;
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             const int n = 32 * i + r;
-            if (n >= nvalid) continue;
+            if (n >= nvalid || (SPLIT && mw == 0)) continue;
             const int route = out_route[i];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -592,7 +621,8 @@ __global__ __launch_bounds__(256, (qmm_lds_occupancy<BITS, GATED, NT>())) void q
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const float g = acc0[i][4 * q + k];
-                    if constexpr (GATED) v[k] = siluf_(g) * acc1[i][4 * q + k];
+                    if constexpr (SPLIT) v[k] = xch[(slab * NT * 16 + i * 16 + 4 * q + k) * 64 + lane] * g;
+                    else if constexpr (GATED) v[k] = siluf_(g) * acc1[i][4 * q + k];
                     else v[k] = g;
                 }
                 const size_t o = (size_t)route * R + m0;
@@ -680,9 +710,13 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         P.rt_groups = (P.row_tiles + rtb - 1) / rtb;
         const size_t lwork = chunks * (size_t)P.rt_groups;
         grid = dim3((unsigned)(8 * ((lwork + 7) / 8)));
+        // 5-bit gated: the split eight-wave form (gate and up on different waves; its
+        // costlier code extraction then overlaps the other wave's MFMAs: 6 % faster on
+        // config 4, while 8-bit gated measured no gain)
 #define DIH_QMM_LDS_CASE(B, GT, N)                                                  \
         if (m0->bits == B && gated == GT && nt == N) {                              \
-            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4>), grid, block, 0, s, P);        \
+            constexpr bool SP = GT && B == 5;                                       \
+            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP>), grid, dim3(SP ? 512 : 256), 0, s, P); \
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }
         DIH_QMM_LDS_CASE(8, true, 2) DIH_QMM_LDS_CASE(8, false, 2) DIH_QMM_LDS_CASE(8, false, 4)

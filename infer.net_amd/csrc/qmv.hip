@@ -8,6 +8,12 @@
 // once per lane per launch. This is the semantics of quant_rows / quant_dot
 // (quantized.mm:83-144) and expert_gate_up (quantized.mm:148-189), re-tiled for wave64.
 //
+// Activations: each block stages its slot's x once in LDS (loads issued before the weight
+// ring, so waiting for them does not wait for weights). With 8-bit codes and bf16 x the
+// copy is f16 (exact for bf16 values below 2^15; a chunk reaching 2^15 is scaled by a
+// power of two) and the dot takes two codes per instruction (chunk_dot_h8); otherwise it
+// is f32. Each chunk also stores the sum of its staged values.
+//
 // Latency hiding: each wave keeps D row groups in flight in a register ring. The raw
 // words of a row group (codes and the bf16 bit patterns of its scales and biases) stay
 // untouched until the group is consumed, and every load is unconditional (row and chunk
@@ -43,9 +49,99 @@ struct RawGroup {
     uint32_t su[GATED ? CPL : 1], bu[GATED ? CPL : 1];
 };
 
-template <int BITS, int CPL, bool GATED, int D>
+// LDS copy of one slot's activations: f16 pieces at xh_dw(c, p) (chunk c, 16-byte piece p
+// rotated by c/2 against bank conflicts), or f32 at xf_at(c, i); then per chunk the sum of
+// the stored values and (f16) its power-of-two scale. Sizes: f16 C*2 + C/8 bytes, f32
+// C*4 + C/8 bytes.
+DIH_DEV int xh_dw(int c, int p) { return c * 16 + 4 * ((p + (c >> 1)) & 3); }
+DIH_DEV int xf_at(int c, int i) { return c * 32 + ((i + 4 * (c & 7)) & 31); }
+
+// This thread's raw activations: columns 8*(t + 256k) .. +8 (bf16: v[k][0]; f32: both).
+template <int CPL>
+struct XStage {
+    uint4 v[CPL][2];
+};
+
+template <int CPL>
+DIH_DEV void xstage_load(XStage<CPL> &X, const QmvSeg &S, int slot) {
+    const int t = threadIdx.x, n8 = S.columns >> 3;
+#pragma unroll
+    for (int k = 0; k < CPL; k++) {
+        int i = t + 256 * k;
+        i = i < n8 ? i : n8 - 1;
+        if (S.x_bf16) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(S.x) + (size_t)slot * S.x_slot_stride);
+            X.v[k][0] = p[i];
+            X.v[k][1] = make_uint4(0, 0, 0, 0);
+        } else {
+            const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const float *>(S.x) + (size_t)slot * S.x_slot_stride);
+            X.v[k][0] = p[2 * i];
+            X.v[k][1] = p[2 * i + 1];
+        }
+    }
+}
+
+// Write the staged activations to LDS; four consecutive threads hold one 32-value chunk.
+template <int CPL, bool XH>
+DIH_DEV void xstage_store(const XStage<CPL> &X, const QmvSeg &S, uint32_t *lds) {
+    const int t = threadIdx.x, n8 = S.columns >> 3, nch = S.columns >> 5;
+    float *sums = reinterpret_cast<float *>(lds) + (XH ? (S.columns >> 1) : S.columns);
+    float *mults = sums + nch;
+#pragma unroll
+    for (int k = 0; k < CPL; k++) {
+        const int i = t + 256 * k, c = i >> 2;
+        float f[8];
+        if (S.x_bf16) {
+            const uint32_t u[4] = {X.v[k][0].x, X.v[k][0].y, X.v[k][0].z, X.v[k][0].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                f[2 * q] = __uint_as_float(u[q] << 16);
+                f[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+            }
+        } else {
+            const uint4 a = X.v[k][0], b = X.v[k][1];
+            f[0] = __uint_as_float(a.x); f[1] = __uint_as_float(a.y); f[2] = __uint_as_float(a.z); f[3] = __uint_as_float(a.w);
+            f[4] = __uint_as_float(b.x); f[5] = __uint_as_float(b.y); f[6] = __uint_as_float(b.z); f[7] = __uint_as_float(b.w);
+        }
+        float sum;
+        if constexpr (XH) {
+            float m = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) m = fmaxf(m, fabsf(f[q]));
+            m = fmaxf(m, dppf<DIH_DPP_XOR1>(m));
+            m = fmaxf(m, dppf<DIH_DPP_XOR2>(m));
+            const int ex = (int)((__float_as_uint(m) >> 23) & 255u) - 126;
+            const int sc = ex > 15 ? ex - 15 : 0;
+            uint32_t pk[4];
+            sum = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const _Float16 h0 = (_Float16)ldexpf(f[2 * q], -sc), h1 = (_Float16)ldexpf(f[2 * q + 1], -sc);
+                sum += (float)h0 + (float)h1;
+                pk[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            }
+            if (i < n8) {
+                *reinterpret_cast<uint4 *>(&lds[xh_dw(c, i & 3)]) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                if ((i & 3) == 0) mults[c] = __uint_as_float((uint32_t)(127 + sc) << 23);
+            }
+        } else {
+            sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+            if (i < n8) {
+                float *xl = reinterpret_cast<float *>(lds);
+                const int i0 = (i & 3) * 8;
+                *reinterpret_cast<float4 *>(&xl[xf_at(c, i0)]) = make_float4(f[0], f[1], f[2], f[3]);
+                *reinterpret_cast<float4 *>(&xl[xf_at(c, i0 + 4)]) = make_float4(f[4], f[5], f[6], f[7]);
+            }
+        }
+        sum += dppf<DIH_DPP_XOR1>(sum);
+        sum += dppf<DIH_DPP_XOR2>(sum);
+        if (i < n8 && (i & 3) == 0) sums[c] = sum;
+    }
+}
+
+template <int BITS, int CPL, bool GATED, int D, bool XH>
 DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_id, int wi, int W,
-                      int K) {
+                      int K, bool active, const XStage<CPL> &X, uint32_t *lds) {
     const int lane = threadIdx.x & 63;
     const int rpw = 64 / lpr;  // rows per row group
     const int g = lane / lpr, j = lane - g * lpr;
@@ -80,35 +176,61 @@ DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_i
     };
 
     RawGroup<BITS, CPL, GATED> ring[D];
+    if (active) {
 #pragma unroll
-    for (int d = 0; d < D; d++) load(ring[d], wi + d * W);
+        for (int d = 0; d < D; d++) load(ring[d], wi + d * W);
+    }
 
-    // This lane's activations and their chunk sums (zero for masked chunks).
-    float xr[CPL][32];
-    float xs[CPL];
-    const void *xb = S.x_bf16
-        ? (const void *)(static_cast<const uint16_t *>(S.x) + (size_t)slot * S.x_slot_stride)
-        : (const void *)(static_cast<const float *>(S.x) + (size_t)slot * S.x_slot_stride);
+    // the block's activations into LDS (every wave of the block takes part), then this
+    // lane's chunks from there
+    xstage_store<CPL, XH>(X, S, lds);
+    __syncthreads();
+    if (!active) return;
+    const float *sums = reinterpret_cast<const float *>(lds) + (XH ? (S.columns >> 1) : S.columns);
+    const float *mults = sums + nchunk;
+    float xr[CPL][XH ? 1 : 32];
+    uint32_t xq[CPL][XH ? 16 : 1];
+    float xs[CPL], xm[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
-        load_x32(xr[c], xb, S.x_bf16, chc[c] * 32);
-        xs[c] = 0.f;
+        xs[c] = sums[chc[c]];
+        if constexpr (XH) {
+            xm[c] = mults[chc[c]];
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            xr[c][i] = valid[c] ? xr[c][i] : 0.f;
-            xs[c] += xr[c][i];
+            for (int p = 0; p < 4; p++) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(&lds[xh_dw(chc[c], p)]);
+                xq[c][4 * p] = v.x; xq[c][4 * p + 1] = v.y; xq[c][4 * p + 2] = v.z; xq[c][4 * p + 3] = v.w;
+            }
+        } else {
+            xm[c] = 1.f;
+            const float *xl = reinterpret_cast<const float *>(lds);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float4 v = *reinterpret_cast<const float4 *>(&xl[xf_at(chc[c], 4 * q)]);
+                xr[c][4 * q] = v.x; xr[c][4 * q + 1] = v.y; xr[c][4 * q + 2] = v.z; xr[c][4 * q + 3] = v.w;
+            }
         }
     }
+
+    // one chunk's affine dot: s*sum(q*x) + b*sum(x)
+    auto dot = [&](const Chunk<BITS> &w, uint32_t sb, uint32_t bb, int c) -> float {
+        if constexpr (XH) {
+            const float d = chunk_dot_h8(reinterpret_cast<const Chunk<8> &>(w), xq[c]) - 1024.f * xs[c];
+            return xm[c] * (bf16_to_f32(sb) * d + bf16_to_f32(bb) * xs[c]);
+        } else {
+            return bf16_to_f32(sb) * chunk_dot<BITS>(w, xr[c]) + bf16_to_f32(bb) * xs[c];
+        }
+    };
 
     auto consume = [&](const RawGroup<BITS, CPL, GATED> &st, int grp) {
         const int r = grp * rpw + g;
         float a = 0.f, b = 0.f;
 #pragma unroll
         for (int c = 0; c < CPL; c++) {
-            const float v = bf16_to_f32(st.s[c]) * chunk_dot<BITS>(st.w[c], xr[c]) + bf16_to_f32(st.b[c]) * xs[c];
+            const float v = dot(st.w[c], st.s[c], st.b[c], c);
             a += valid[c] ? v : 0.f;
             if constexpr (GATED) {
-                const float vu = bf16_to_f32(st.su[c]) * chunk_dot<BITS>(st.u[c], xr[c]) + bf16_to_f32(st.bu[c]) * xs[c];
+                const float vu = dot(st.u[c], st.su[c], st.bu[c], c);
                 b += valid[c] ? vu : 0.f;
             }
         }
@@ -138,6 +260,7 @@ DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_i
 
 template <int BITS, int CPL, int D>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
+    extern __shared__ __align__(16) uint32_t qx[];   // the block's staged activations
     const int blk = blockIdx.x;
     int k = 0;
 #pragma unroll
@@ -148,8 +271,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     const int slot = local / P.blocks_per_slot[k];
     const int wi = (local - slot * P.blocks_per_slot[k]) * 4 + (threadIdx.x >> 6);
     const int W = P.waves_per_slot[k];
-    if (wi >= W) return;
+    // waves past the slot's rows still stage activations and meet the block barrier
+    const bool active = wi < W;
     const int lane = threadIdx.x & 63;
+    XStage<CPL> X;
+    xstage_load<CPL>(X, S, slot);
 
     // Expert of this slot: a device id, or top-8 of the router logits computed by this
     // wave (the first wave of the segment publishes ids/probs for the next kernel).
@@ -173,10 +299,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     }
     const bool bad_id = e >= (uint32_t)S.experts;
     if (bad_id) e = 0u;
-    if (S.p1)
-        qmv_wave<BITS, CPL, true, D>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k]);
-    else
-        qmv_wave<BITS, CPL, false, D>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k]);
+    const bool xh = BITS == 8 && S.x_bf16;   // uniform over the block
+    if (S.p1) {
+        if (xh) qmv_wave<BITS, CPL, true, D, BITS == 8>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+        else qmv_wave<BITS, CPL, true, D, false>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+    } else {
+        if (xh) qmv_wave<BITS, CPL, false, D, BITS == 8>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+        else qmv_wave<BITS, CPL, false, D, false>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+    }
 }
 
 static int pow2ceil(int v) {
@@ -236,9 +366,13 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
         depth = 1;
     }
     dim3 grid(blocks), block(256);
+    // staged activations: f32 (4 B per column) plus per-chunk sum and scale
+    int maxc = 0;
+    for (int i = 0; i < nseg; i++) maxc = std::max(maxc, segs[i].columns);
+    const uint32_t lds = (uint32_t)maxc * 4 + (uint32_t)(maxc / 32) * 8;
 #define DIH_QMV_CASE(B, C, D)                                                  \
     if (bits == B && cpl <= C && depth == D) {                                  \
-        DIH_LAUNCH((qmv_kernel<B, C, D>), grid, block, 0, s, P);               \
+        DIH_LAUNCH((qmv_kernel<B, C, D>), grid, block, lds, s, P);             \
         return hip_ok(hipGetLastError(), error, capacity, "qmv launch");       \
     }
     DIH_QMV_CASE(8, 1, 1) DIH_QMV_CASE(8, 1, 2) DIH_QMV_CASE(8, 1, 4)

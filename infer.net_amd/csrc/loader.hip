@@ -10,9 +10,9 @@
 // Failures report -1 (invalid data, the reference's InvalidDataException) or -2
 // (unsupported, NotSupportedException) plus the reference's message text.
 //
-// Upload: each tensor is read with pread into one of two pinned 64 MiB staging buffers
-// while the other is copied to the device on the checkpoint's own stream, so disk or page
-// cache reads overlap the PCIe copies. No host-side staging copy of the whole matrix is
+// Upload: each tensor is read with pread (up to eight threads per 64 MiB piece) into one of
+// two pinned 64 MiB staging buffers while the other is copied to the device on the
+// checkpoint's own stream, so disk or page cache reads overlap the PCIe copies. No host-side staging copy of the whole matrix is
 // kept (the reference writes into unified memory in place, QuantizedMetal.cs:177).
 #include <fcntl.h>
 #include <string.h>
@@ -20,8 +20,10 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <memory>
+#include <thread>
 #include <new>
 #include <string>
 #include <unordered_map>
@@ -76,6 +78,28 @@ bool read_all(int fd, void *dst, size_t bytes, int64_t offset) {
         offset += n;
     }
     return true;
+}
+
+// Large reads in up to eight parallel pread streams (page-cache copies are bounded by one
+// thread's memcpy rate; NVMe reads by queue depth).
+bool read_parallel(int fd, void *dst, size_t bytes, int64_t offset) {
+    constexpr size_t kPart = (size_t)8 << 20;
+    const int parts = (int)std::min<size_t>(8, (bytes + kPart - 1) / kPart);
+    if (parts <= 1) return read_all(fd, dst, bytes, offset);
+    const size_t per = ((bytes + parts - 1) / parts + 4095) & ~(size_t)4095;
+    std::atomic<bool> ok{true};
+    std::vector<std::thread> th;
+    for (int i = 1; i < parts; i++) {
+        const size_t b = per * (size_t)i;
+        if (b >= bytes) break;
+        const size_t n = std::min(per, bytes - b);
+        th.emplace_back([&, b, n] {
+            if (!read_all(fd, static_cast<char *>(dst) + b, n, offset + (int64_t)b)) ok = false;
+        });
+    }
+    if (!read_all(fd, dst, std::min(per, bytes), offset)) ok = false;
+    for (auto &x : th) x.join();
+    return ok;
 }
 
 int dtype_code(const std::string &d) {
@@ -357,7 +381,7 @@ bool ck_upload(Checkpoint &c, int device, const StFile *s, const StTensor *t, vo
     for (int k = 0; off < t->bytes; k ^= 1) {
         const size_t n = (size_t)std::min<int64_t>((int64_t)kStageBytes, t->bytes - off);
         if (!hip_ok(hipEventSynchronize(c.done[k]), e, sizeof(e), "staging wait")) return f.set(kInvalid, e);
-        if (!read_all(s->fd, c.stage[k], n, t->start + off)) return f.set(kInvalid, "Tensor read failed.");
+        if (!read_parallel(s->fd, c.stage[k], n, t->start + off)) return f.set(kInvalid, "Tensor read failed.");
         if (!hip_ok(hipMemcpyAsync(static_cast<char *>(dst) + off, c.stage[k], n, hipMemcpyHostToDevice, c.stream), e,
                     sizeof(e), "weight upload") ||
             !hip_ok(hipEventRecord(c.done[k], c.stream), e, sizeof(e), "staging record"))

@@ -286,6 +286,36 @@ class Bench:
         return {"tokens": T, "per_matrix": out, "TFLOP_s": tot_f / (tot_ms * 1e-3) / 1e12,
                 "mfma_frac": tot_f / (tot_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
+    def dense_small(self, steps, warmup, copies=16):
+        """Dense projection at short chunks (the GEMV-vs-GEMM dispatch policy of p_gemv,
+        gpu_prefill.mm:603-620): q/gate [8192 x 2048] 8-bit at T = 1..64, weights rotated
+        over `copies` (285 MB, beyond the MALL). Times dih_dense and, for comparison, the
+        batched GEMV (dih_qmv over T <= 8 slots of expert 0)."""
+        torch, dh = self.torch, self.dh
+        R, C = 8192, 2048
+        mats = [self.matrix(1, R, C, 8) for _ in range(copies)]
+        out = {}
+        for T in (1, 2, 4, 8, 16, 32, 64):
+            x = self.bf16(T, C)
+            y = torch.zeros((T, R), dtype=torch.bfloat16, device="cuda")
+            ids = torch.zeros(T, dtype=torch.int32, device="cuda")
+            res = {}
+            for path in (("dense", "qmv") if T <= 8 else ("dense",)):
+                def step(i, x=x, y=y, T=T, path=path):
+                    m = mats[i % copies]
+                    if path == "dense":
+                        dh.dense(self.dev, m, T, x, y, y_dtype=dh.BF16)
+                    else:
+                        dh.qmv(self.dev, m, x, y, experts=ids if T > 1 else None, count=T, batched=True,
+                               y_dtype=dh.BF16)
+                ms, _ = self.timed_graph(step, max(8, steps // 2), min(warmup, 4))
+                res[path] = {"us": ms * 1e3, "GB_s": qbytes(1, R, C, 8) / (ms * 1e-3) / 1e9}
+            out[T] = res
+            del x, y
+        for m in mats:
+            m.dispose()
+        return out
+
     def lm_head(self, steps, warmup, copies=2):
         """Config 5b: lm_head [248320 x 2048] 8-bit in 4 vocab slices, f32 logits, argmax."""
         torch, dh = self.torch, self.dh
@@ -439,6 +469,11 @@ def main():
     if "load" in wls:
         res["load"] = b.load()
         log(f"[load] {res['load']['GB_s']:.1f} GB/s ({res['load']['bytes'] / 1e6:.0f} MB in {res['load']['ms']:.1f} ms)")
+    if "dense_small" in wls:
+        res["dense_small"] = b.dense_small(steps, warmup)
+        for T, r in res["dense_small"].items():
+            q = f", batched qmv {r['qmv']['us']:.1f} us" if "qmv" in r else ""
+            log(f"[dense_small] T={T}: dense {r['dense']['us']:.1f} us{q}")
     if "copycal" in wls:
         print(json.dumps(b.copycal(max(1, min(steps, 8)))), flush=True)
         return

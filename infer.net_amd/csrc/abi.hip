@@ -912,11 +912,24 @@ __attribute__((visibility("default"))) int dih_dense(void *ctx, void *matrix, in
         return -1;
     }
     if (!sync_matrix(m, error, capacity)) return -1;
+    hipStream_t s = pick(c, stream);
+    ProfScope prof_scope(c);
+    // Dispatch policy (p_gemv, gpu_prefill.mm:603-620, picks GEMV kernels below 64 tokens):
+    // up to kDenseGemvTokens tokens run as one batched GEMV launch (each token a slot of
+    // expert 0; measured 8 / 13 / 18 us against 26 us for the MFMA tile at 1 / 2 / 4 tokens
+    // of an 8192 x 2048 8-bit matrix), longer chunks as the MFMA GEMM.
+    constexpr int kDenseGemvTokens = 4;
+    if (tokens <= kDenseGemvTokens) {
+        QmvSeg sg = seg_of(m);
+        sg.count = tokens; sg.x = x; sg.x_bf16 = 1; sg.x_slot_stride = m->columns;
+        sg.y = y; sg.y_bf16 = y_dtype == DIH_BF16;
+        bool ok = launch_qmv(&sg, 1, m->bits, nullptr, s, error, capacity);
+        prof_mark(c, s, "dense_qmm");
+        return ok ? 0 : -1;
+    }
     QmmArgs a;
     a.m0 = m; a.tokens = tokens; a.dense = 1; a.x = static_cast<const uint16_t *>(x); a.in_mode = 0;
     a.y = y; a.y_bf16 = y_dtype == DIH_BF16;
-    hipStream_t s = pick(c, stream);
-    ProfScope prof_scope(c);
     bool ok = launch_qmm(a, s, error, capacity);
     prof_mark(c, s, "dense_qmm");
     return ok ? 0 : -1;

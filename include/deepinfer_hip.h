@@ -237,6 +237,35 @@ int dih_moe_prefill_norm(void *context, const dih_moe_layer *layer, int tokens, 
 int dih_dense(void *context, void *matrix, int tokens, const void *x, void *y, int y_dtype,
               void *stream, char *error, int capacity);
 
+/* Causal GQA attention of `tokens` query tokens at cache positions position ..
+ * position+tokens-1, with the output gate: the BF16 prefill attention and its partition
+ * combine (prefill_attention_bf16.mm:13-55, graph_attention_combine gpu_graph.mm:177-213),
+ * dispatched by p_fused_attention (gpu_prefill.mm:552-570) for a prefill chunk and by
+ * g_try_fused_attention (gpu_prefill.mm:579-584) for one decode token. Geometry is the
+ * model's: 16 query heads over 2 KV heads, head dim 256.
+ *   q       [tokens][16][256] f32 or bf16 (q_dtype): normed, rotated queries
+ *   keys, values  bf16 cache [cache_positions][2][256]; rows 0..position+tokens-1 hold keys
+ *           and values of this chunk and everything before it
+ *   gate    [tokens][16][512] f32 or bf16: the q projection output; head h's gate values
+ *           sit at h*512+256 .. h*512+511
+ *   out     [tokens][16][256] f32 or bf16:
+ *           softmax(q.k/16 over keys 0..position+t) . v * sigmoid(gate)
+ *   partition  keys per partition, a multiple of 32; 0 lets the library choose. Keys are
+ *           scanned in 32-key blocks; probabilities are rounded to bf16 per block against
+ *           the running maximum of their partition, as the reference rounds them.
+ * Device pointers; runs on `stream` (NULL: the context's stream). Returns 0, or -1 with a
+ * message when an argument is invalid (nothing is launched then). */
+int dih_attention(void *context, const void *q, int q_dtype, const uint16_t *keys,
+                  const uint16_t *values, int cache_positions, const void *gate, int gate_dtype,
+                  void *out, int out_dtype, int position, int tokens, int partition,
+                  void *stream, char *error, int capacity);
+
+/* The partition size dih_attention uses for these arguments (`partition` itself when it
+ * is positive, else the library's choice); -1 for invalid arguments. The partition sets
+ * where probabilities are rounded (see dih_attention) and the partial-result scratch:
+ * tokens * 16 * ceil((position + tokens) / partition) * 1032 bytes when above one. */
+int dih_attention_partition(int position, int tokens, int partition);
+
 /* Per-stage GPU timing (the reference's DEEPINFER_METAL_GPU_PROFILE per-dispatch
  * timestamps, gpu_graph.mm:329-338, as a runtime switch instead of getenv). While enabled,
  * every device-resident call records HIP events on its own stream between its kernels.

@@ -935,6 +935,45 @@ __attribute__((visibility("default"))) int dih_dense(void *ctx, void *matrix, in
     return ok ? 0 : -1;
 }
 
+__attribute__((visibility("default"))) int dih_attention(void *ctx, const void *q, int q_dtype,
+                                                         const uint16_t *keys, const uint16_t *values,
+                                                         int cache_positions, const void *gate, int gate_dtype,
+                                                         void *out, int out_dtype, int position, int tokens,
+                                                         int partition, void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    auto dtype_ok = [](int d) { return d == DIH_F32 || d == DIH_BF16; };
+    if (!c || !q || !keys || !values || !gate || !out || !dtype_ok(q_dtype) || !dtype_ok(gate_dtype) ||
+        !dtype_ok(out_dtype) || tokens < 1 || position < 0 || cache_positions < 1 ||
+        (int64_t)position + tokens > cache_positions || partition < 0 || partition % 32 != 0) {
+        set_error(error, capacity, "Invalid attention arguments");
+        return -1;
+    }
+    const int part = attention_partition(position, tokens, partition);
+    const size_t nparts = ((size_t)position + tokens + part - 1) / part;
+    AttentionArgs a;
+    a.q = q; a.q_bf16 = q_dtype == DIH_BF16;
+    a.keys = keys; a.values = values;
+    a.gate = gate; a.gate_bf16 = gate_dtype == DIH_BF16;
+    a.out = out; a.out_bf16 = out_dtype == DIH_BF16;
+    a.position = position; a.tokens = tokens; a.partition = part;
+    if (nparts > 1) {
+        const size_t rows = (size_t)tokens * 16 * nparts;
+        a.pacc = static_cast<float *>(scratch(c, S_APART, rows * 256 * 4, error, capacity));
+        a.pstat = static_cast<float *>(scratch(c, S_ASTAT, rows * 8, error, capacity));
+        if (!a.pacc || !a.pstat) return -1;
+    }
+    hipStream_t s = pick(c, stream);
+    ProfScope prof_scope(c);
+    bool ok = launch_attention(a, s, error, capacity);
+    prof_mark(c, s, "attention");
+    return ok ? 0 : -1;
+}
+
+__attribute__((visibility("default"))) int dih_attention_partition(int position, int tokens, int partition) {
+    if (tokens < 1 || position < 0 || partition < 0 || partition % 32 != 0) return -1;
+    return attention_partition(position, tokens, partition);
+}
+
 __attribute__((visibility("default"))) int dih_set_profiling(void *ctx, int enabled) {
     Context *c = as_ctx(ctx);
     if (!c) return -1;

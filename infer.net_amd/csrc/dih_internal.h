@@ -60,7 +60,7 @@ struct Context {
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_TICKETS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_CAND, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_COUNT_
 };
 
 // Error helpers (bridge.mm:9-15 convention).
@@ -198,5 +198,22 @@ bool launch_dequant_bf16(const Matrix *m, int expert, uint16_t *out, hipStream_t
                          int capacity);
 bool launch_embedding(const Matrix *m, int token, float *out, hipStream_t s, char *error,
                       int capacity);
+
+// Causal GQA attention over a bf16 KV cache (attention.hip). Geometry 16 query heads,
+// 2 KV heads, head dim 256; `partition` keys per partition (a multiple of 32). With more
+// than one partition, pacc [tokens*16*nparts*256] f32 and pstat [tokens*16*nparts] float2
+// hold the partition results, nparts = ceil((position + tokens) / partition).
+struct AttentionArgs {
+    const void *q = nullptr; int q_bf16 = 0;
+    const uint16_t *keys = nullptr, *values = nullptr;
+    const void *gate = nullptr; int gate_bf16 = 0;
+    void *out = nullptr; int out_bf16 = 0;
+    float *pacc = nullptr; float *pstat = nullptr;
+    int position = 0, tokens = 0, partition = 0;
+};
+// Partition size for a call: `requested` when positive, else enough partitions that the
+// blocks fill the GPU.
+int attention_partition(int position, int tokens, int requested);
+bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity);
 
 }  // namespace dih

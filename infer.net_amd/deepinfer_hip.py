@@ -83,7 +83,8 @@ EXPORTS = [
     "dih_quant_batch", "dih_quant_matvec", "dih_quant_experts", "dih_quant_embedding",
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
     "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm",
-    "dih_moe_prefill_norm", "dih_dense", "dih_set_profiling",
+    "dih_moe_prefill_norm", "dih_dense", "dih_attention",
+    "dih_attention_partition", "dih_set_profiling",
     "dih_profile_read", "dih_version",
     "dih_safetensors_open", "dih_safetensors_close", "dih_safetensors_count",
     "dih_safetensors_info", "dih_safetensors_get", "dih_safetensors_read",
@@ -135,6 +136,8 @@ def load():
         "dih_moe_decode_norm": ([P, P, P, P, P, P, P, P, E, I], I),
         "dih_moe_prefill_norm": ([P, P, I, P, P, I, P, P, P, P, E, I], I),
         "dih_dense": ([P, P, I, P, P, I, P, E, I], I),
+        "dih_attention": ([P, P, I, P, P, I, P, I, P, I, I, I, I, P, E, I], I),
+        "dih_attention_partition": ([I, I, I], I),
         "dih_set_profiling": ([P, I], I),
         "dih_profile_read": ([P, P, P, P, I], I),
         "dih_version": ([], ctypes.c_char_p),
@@ -544,6 +547,26 @@ def dense(dev, m, tokens, x, y, y_dtype=F32, stream=None) -> None:
     err = _errbuf()
     _check(dev._lib.dih_dense(_ctx(dev), m.handle, tokens, _dp(x), _dp(y), y_dtype, _stream(stream), err, _ERR),
            err, ArgumentError)
+
+
+def attention(dev, q, keys, values, gate, out, position, tokens, partition=0, q_dtype=F32,
+              gate_dtype=F32, out_dtype=F32, cache_positions=None, stream=None) -> None:
+    """Causal GQA attention with the output gate (dih_attention; p_fused_attention,
+    gpu_prefill.mm:552-570). keys/values: bf16 cache tensors [cache_positions, 512]."""
+    if cache_positions is None:
+        cache_positions = keys.shape[0]
+    err = _errbuf()
+    _check(dev._lib.dih_attention(_ctx(dev), _dp(q), q_dtype, _dp(keys), _dp(values), cache_positions,
+                                  _dp(gate), gate_dtype, _dp(out), out_dtype, position, tokens, partition,
+                                  _stream(stream), err, _ERR), err, ArgumentError)
+
+
+def attention_partition(position, tokens, partition=0) -> int:
+    """Keys per partition dih_attention uses for these arguments."""
+    n = load().dih_attention_partition(position, tokens, partition)
+    if n < 0:
+        raise ArgumentError("Invalid attention arguments")
+    return n
 
 
 def set_profiling(dev, enabled: bool) -> None:

@@ -413,3 +413,20 @@ ORC_API int orc_openmp_threads(void) {
     return 1;
 #endif
 }
+
+/* ---------------------------------------------------------------- attention inputs
+ * The reference's attention checks draw every input from one xorshift32 stream
+ * (shifts 13, 17, 5) mapped to value = (int)(s % 10001) - 5000) / 12500 in f32
+ * (prefill_attention_checks.mm:17-18; attention_batch_checks.mm:19). `interleave` > 1
+ * deals consecutive draws round-robin into that many output arrays, as the checks fill
+ * keys and values from one stream (prefill_attention_checks.mm:20-24). */
+ORC_API uint32_t orc_xorshift_fill(uint32_t seed, float *const *out, int interleave, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        for (int k = 0; k < interleave; k++) {
+            seed ^= seed << 13;
+            seed ^= seed >> 17;
+            seed ^= seed << 5;
+            out[k][i] = (float)((int)(seed % 10001u) - 5000) / 12500.0f;
+        }
+    return seed;
+}

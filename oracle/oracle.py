@@ -73,6 +73,8 @@ def _declare(L):
     L.orc_cpu_moe_token.argtypes = [ctypes.POINTER(OrcMoeLayer), P, P, I]
     L.orc_cpu_moe_token.restype = I
     L.orc_openmp_threads.restype = I
+    L.orc_xorshift_fill.argtypes = [ctypes.c_uint32, P, I, ctypes.c_size_t]
+    L.orc_xorshift_fill.restype = ctypes.c_uint32
 
 
 def _ptr(a: np.ndarray):
@@ -274,6 +276,107 @@ def merge_norm_f64(residual, y, weight=None, epsilon=1e-6, residual_bf16=False):
         return stored, None
     inv = 1.0 / np.sqrt(np.mean(stored * stored, axis=1, keepdims=True) + float(epsilon))
     return stored, stored * inv * np.asarray(weight, dtype=np.float64)[None, :]
+
+
+# ---------------------------------------------------------------- attention (numpy)
+# Full-attention layer geometry (Qwen3.6-35B-A3B as the reference hard-codes it):
+# 16 query heads share 2 KV heads (8 per group), head dim 256; the KV cache holds
+# [position][kv head][256] bf16 (stride 512), the q projection output [token][16][512]
+# interleaves each head's 256 query values with its 256 output-gate values
+# (gpu_graph.mm:199-213; prefill_attention_bf16.mm:13-14, 34, 48).
+ATT_HEADS, ATT_KV_HEADS, ATT_DIM = 16, 2, 256
+
+
+def xorshift_values(seed: int, n: int, interleave: int = 1):
+    """Inputs as the reference's attention checks draw them (orc_xorshift_fill):
+    returns ([f32[n]] * interleave, next seed)."""
+    outs = [np.zeros(n, dtype=np.float32) for _ in range(interleave)]
+    ptrs = (ctypes.c_void_p * interleave)(*[o.ctypes.data for o in outs])
+    seed = lib().orc_xorshift_fill(ctypes.c_uint32(seed), ptrs, interleave, n)
+    return outs, int(seed)
+
+
+def _attention_rows(S, V, partition, key_tile, round_probs):
+    """Online softmax over one KV head for rows of scores S [R, n] (masked keys -inf)
+    against values V [n, 256], exactly as the reference's double oracle forms it
+    (prefill_attention_checks.mm:59-67, the arithmetic of prefill_attention_bf16.mm:32-54
+    and graph_attention_combine gpu_graph.mm:199-213): partitions of `partition` keys,
+    each scanned in `key_tile`-key blocks with a running maximum; the block's
+    probabilities exp(s - max) enter the partition sum unrounded and the value product
+    rounded to bf16 (through f32) when `round_probs`; partitions are combined against
+    the global maximum. Returns the normalized [R, 256]."""
+    R, n = S.shape
+    with np.errstate(invalid="ignore", over="ignore"):
+        M = np.max(S, axis=1)
+        total = np.zeros(R)
+        weighted = np.zeros((R, V.shape[1]))
+        for start in range(0, n, partition):
+            pm = np.full(R, -np.inf)
+            psum = np.zeros(R)
+            num = np.zeros((R, V.shape[1]))
+            for block in range(start, min(start + partition, n), key_tile):
+                end = min(block + key_tile, start + partition, n)
+                Sb = S[:, block:end]
+                nxt = np.maximum(pm, np.max(Sb, axis=1))
+                alpha = np.where(np.isfinite(pm), np.exp(pm - nxt), 0.0)
+                psum *= alpha
+                num *= alpha[:, None]
+                P = np.where(np.isfinite(Sb), np.exp(Sb - nxt[:, None]), 0.0)
+                psum += P.sum(axis=1)
+                if round_probs:
+                    P = round_bf16(P.astype(np.float32)).astype(np.float64)
+                num += P @ V[block:end]
+                pm = nxt
+            scale = np.where(np.isfinite(pm), np.exp(pm - M), 0.0)
+            total += scale * psum
+            weighted += scale[:, None] * num
+    return weighted / total[:, None]
+
+
+def attention_f64(q, keys, values, gate_raw, position, bf16_operands=True, partition=1024,
+                  key_tile=32, round_probs=None):
+    """Causal GQA attention of a chunk of `T` query tokens at cache positions
+    position..position+T-1 with the output gate, in float64.
+
+    q f32 [T, 16*256] (normed and rotated queries); keys/values [>= position+T, 512]
+    (the bf16 cache's values as f32); gate_raw [T, 8192] (q projection output, head h's
+    gate at h*512+256+d). Token t attends keys 0..position+t with scores q.k/16
+    (prefill_attention_bf16.mm:39); out[t, h*256+d] = softmax-weighted values times
+    sigmoid(gate) (gpu_graph.mm:212).
+
+    bf16_operands=True is the reference's BF16 path as its own double oracle states it
+    (prefill_attention_checks.mm:53, 57-67): q rounded to bf16 (RNE), probabilities
+    rounded per key block (see _attention_rows; partition/key_tile select the blocks).
+    bf16_operands=False is the plain softmax of the fp32 path (:68-69)."""
+    q = np.asarray(q, dtype=np.float32)
+    T = q.shape[0]
+    n = position + T
+    D = ATT_DIM
+    K = np.asarray(keys[:n], dtype=np.float64).reshape(n, ATT_KV_HEADS, D)
+    V = np.asarray(values[:n], dtype=np.float64).reshape(n, ATT_KV_HEADS, D)
+    qq = (round_bf16(q) if bf16_operands else q).astype(np.float64).reshape(T, ATT_HEADS, D)
+    if round_probs is None:
+        round_probs = bf16_operands
+    group = ATT_HEADS // ATT_KV_HEADS
+    out = np.zeros((T, ATT_HEADS, D))
+    last = position + np.arange(T)
+    for kh in range(ATT_KV_HEADS):
+        Q = qq[:, kh * group:(kh + 1) * group, :].reshape(T * group, D)
+        rows_last = np.repeat(last, group)
+        for r0 in range(0, T * group, 1024):
+            r1 = min(r0 + 1024, T * group)
+            S = (Q[r0:r1] @ K[:, kh, :].T) / 16.0
+            S[np.arange(n)[None, :] > rows_last[r0:r1, None]] = -np.inf
+            if bf16_operands or round_probs:
+                res = _attention_rows(S, V[:, kh, :], partition, key_tile, round_probs)
+            else:
+                m = np.max(S, axis=1, keepdims=True)
+                P = np.exp(S - m)
+                res = (P @ V[:, kh, :]) / P.sum(axis=1, keepdims=True)
+            out.reshape(T * ATT_HEADS, D)[np.arange(r0, r1) // group * ATT_HEADS
+                                          + kh * group + np.arange(r0, r1) % group] = res
+    gate = np.asarray(gate_raw, dtype=np.float64).reshape(T, ATT_HEADS, 2 * D)[:, :, D:]
+    return (out / (1.0 + np.exp(-gate))).reshape(T, ATT_HEADS * D)
 
 
 def cpu_qmv(m: QMatrix, x, experts=None, batched=False, threads=1) -> np.ndarray:

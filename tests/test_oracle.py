@@ -302,3 +302,120 @@ def test_merge_norm_closed_forms():
     # f32 storage: the sum is rounded to f32 before the norm
     s, _ = orc.merge_norm_f64(np.array([[1.0]]), np.array([[2.0 ** -30]]))
     assert s.tolist() == [[1.0]]
+
+
+# ---------------------------------------------------------------- attention
+
+def _xorshift_py(seed, n):
+    out = []
+    for _ in range(n):
+        seed ^= (seed << 13) & 0xFFFFFFFF
+        seed ^= seed >> 17
+        seed ^= (seed << 5) & 0xFFFFFFFF
+        out.append(np.float32((int(seed % 10001) - 5000)) / np.float32(12500.0))
+    return np.array(out, dtype=np.float32), seed
+
+
+def test_xorshift_generator():
+    """orc_xorshift_fill against a pure-Python restatement of prefill_attention_checks.mm:18,
+    including the interleaved key/value fill of :20-24."""
+    (a,), s = orc.xorshift_values(0x6a51c9e7, 300)
+    b, s2 = _xorshift_py(0x6a51c9e7, 300)
+    assert np.array_equal(a, b) and s == s2
+    (k, v), _ = orc.xorshift_values(s, 50, 2)
+    c, _ = _xorshift_py(s, 100)
+    assert np.array_equal(k, c[0::2]) and np.array_equal(v, c[1::2])
+    assert np.all(np.abs(a) <= 0.4)
+
+
+def _attention_inputs(T, position, seed=3):
+    rng = np.random.default_rng(seed)
+    n = position + T
+    q = rng.uniform(-0.4, 0.4, size=(T, 4096)).astype(np.float32)
+    k = orc.round_bf16(rng.uniform(-0.4, 0.4, size=(n, 512)).astype(np.float32))
+    v = orc.round_bf16(rng.uniform(-0.4, 0.4, size=(n, 512)).astype(np.float32))
+    g = rng.uniform(-2, 2, size=(T, 8192)).astype(np.float32)
+    return q, k, v, g
+
+
+def test_attention_zero_queries_closed_form():
+    """bf16_attention_long_checks.mm:13,20: q = 0 makes every score 0, so each head
+    averages its KV head's values; with values 1 / -2 and gates 0 the output is .5 / -1."""
+    T, position = 6, 45
+    v = np.where(np.arange(512) < 256, 1.0, -2.0)[None, :].repeat(position + T, 0)
+    for part, tile in ((1024, 32), (16, 4)):
+        out = orc.attention_f64(np.zeros((T, 4096)), np.zeros_like(v), v, np.zeros((T, 8192)), position,
+                                partition=part, key_tile=tile)
+        assert np.all(out[:, :2048] == 0.5) and np.all(out[:, 2048:] == -1.0)
+
+
+def test_attention_single_key():
+    """The first token of an empty cache sees one key: out = v * sigmoid(gate), whatever q."""
+    q, k, v, g = _attention_inputs(1, 0)
+    out = orc.attention_f64(q, k, v, g, 0).reshape(16, 256)
+    gate = g.reshape(16, 512)[:, 256:].astype(np.float64)
+    want = v[0].reshape(2, 256).astype(np.float64)[np.arange(16) // 8] / (1 + np.exp(-gate))
+    assert np.allclose(out, want, rtol=1e-15, atol=0)
+
+
+def _softmax_loops(q, k, v, g, position):
+    """Brute force over (token, head) with scipy's softmax (independent of the oracle's
+    vectorized masking and head grouping)."""
+    from scipy.special import softmax
+    T = q.shape[0]
+    out = np.zeros((T, 16, 256))
+    for t in range(T):
+        for h in range(16):
+            kh = h // 8
+            keys = k[:position + t + 1, kh * 256:(kh + 1) * 256].astype(np.float64)
+            s = keys @ q[t, h * 256:(h + 1) * 256].astype(np.float64) / 16
+            p = softmax(s)
+            out[t, h] = p @ v[:position + t + 1, kh * 256:(kh + 1) * 256]
+            out[t, h] *= 1 / (1 + np.exp(-g[t, h * 512 + 256:(h + 1) * 512].astype(np.float64)))
+    return out.reshape(T, 4096)
+
+
+def test_attention_plain_softmax_brute_force():
+    q, k, v, g = _attention_inputs(5, 11)
+    want = _softmax_loops(q, k, v, g, 11)
+    got = orc.attention_f64(q, k, v, g, 11, bf16_operands=False)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-15)
+    # q rounded to bf16, probabilities unrounded: the same softmax over rounded queries
+    got = orc.attention_f64(q, k, v, g, 11, bf16_operands=True, round_probs=False)
+    assert np.allclose(got, _softmax_loops(orc.round_bf16(q), k, v, g, 11), rtol=1e-12, atol=1e-15)
+
+
+@pytest.mark.parametrize("partition,tile", [(1024, 32), (64, 32), (32, 32), (7, 3), (5, 5)])
+def test_attention_online_recurrence(partition, tile):
+    """Without probability rounding the partitioned online softmax equals the softmax for
+    any partition and key block (a missed rescale or a wrong combine fails this)."""
+    q, k, v, g = _attention_inputs(9, 70, seed=8)
+    exact = orc.attention_f64(orc.round_bf16(q), k, v, g, 70, bf16_operands=False)
+    got = orc.attention_f64(q, k, v, g, 70, partition=partition, key_tile=tile, round_probs=False)
+    assert np.allclose(got, exact, rtol=1e-11, atol=1e-14)
+
+
+def test_attention_probability_rounding():
+    """Rounding each probability to bf16 moves it by at most 2^-9 relative; the output
+    moves by at most 2^-9 * max|v| * sigmoid(gate), and does move (the rounding is real)."""
+    q, k, v, g = _attention_inputs(12, 200, seed=9)
+    unrounded = orc.attention_f64(q, k, v, g, 200, round_probs=False)
+    rounded = orc.attention_f64(q, k, v, g, 200)
+    d = np.abs(rounded - unrounded)
+    assert np.max(d) <= 2.0 ** -9 * np.max(np.abs(v)) and np.max(d) > 1e-7
+    # the rounding points depend on the key blocks: another block size changes the result
+    other = orc.attention_f64(q, k, v, g, 200, key_tile=64)
+    assert np.max(np.abs(other - rounded)) > 1e-8
+
+
+def test_attention_causal_mask():
+    """Row t reads keys 0..position+t only: changing key/value rows past that leaves the
+    row unchanged and changes the later rows."""
+    q, k, v, g = _attention_inputs(4, 20, seed=10)
+    base = orc.attention_f64(q, k, v, g, 20)
+    k2, v2 = k.copy(), v.copy()
+    k2[22:] += 0.25
+    v2[22:] -= 0.5
+    moved = orc.attention_f64(q, k2, v2, g, 20)
+    assert np.array_equal(base[:2], moved[:2])
+    assert np.all(np.max(np.abs(base[2:] - moved[2:]), axis=1) > 1e-3)

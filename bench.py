@@ -316,6 +316,42 @@ class Bench:
             m.dispose()
         return out
 
+    def attention(self, steps, warmup):
+        """Full-attention layer (prefill_attention_bf16 + combine; p_fused_attention,
+        gpu_prefill.mm:552-570): 16 query heads over 2 KV heads, head dim 256, bf16 cache.
+        Cases: a 2048-token chunk on an empty cache, the last 2048-token chunk of a 32K
+        prompt, and one decode token at 32K. FLOPs count the causal work only: 1024 per
+        (query row, visible key) (q.k and p.v, 2 x 256 multiply-adds)."""
+        torch, dh = self.torch, self.dh
+        out = {}
+        for name, position, T in (("chunk2048_pos0", 0, 2048), ("chunk2048_pos30720", 30720, 2048),
+                                  ("decode_pos32767", 32767, 1)):
+            cap = position + T
+            g = torch.Generator(device="cuda").manual_seed(5)
+            keys = (torch.rand((cap, 512), device="cuda", generator=g) * 0.8 - 0.4).to(torch.bfloat16)
+            vals = (torch.rand((cap, 512), device="cuda", generator=g) * 0.8 - 0.4).to(torch.bfloat16)
+            q = torch.rand((T, 4096), device="cuda", generator=g) * 0.8 - 0.4
+            raw = torch.rand((T, 8192), device="cuda", generator=g) * 4 - 2
+            y = torch.zeros((T, 4096), device="cuda")
+
+            def step(i, q=q, keys=keys, vals=vals, raw=raw, y=y, position=position, T=T):
+                dh.attention(self.dev, q, keys, vals, raw, y, position, T)
+
+            n = max(4, steps // 12) if T > 1 else max(16, steps)
+            ms, prof = self.timed_graph(step, n, min(warmup, 3))
+            tot, cnt = prof.get("attention", (0, 1))
+            ctot, ccnt = prof.get("attention_combine", (0, 1))
+            visible = T * position + T * (T + 1) // 2
+            flops = 1024.0 * 16 * visible
+            kv_bytes = 2 * cap * 512 * 2
+            out[name] = {"position": position, "tokens": T, "partition": dh.attention_partition(position, T),
+                         "ms": ms, "GFLOP": flops / 1e9, "TFLOP_s": flops / (ms * 1e-3) / 1e12,
+                         "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         "kv_GB_s": kv_bytes / (ms * 1e-3) / 1e9, "attn_kernel_avg_us": tot / max(cnt, 1) * 1e3,
+                         "combine_avg_us": ctot / max(ccnt, 1) * 1e3}
+            del keys, vals, q, raw, y
+        return out
+
     def lm_head(self, steps, warmup, copies=2):
         """Config 5b: lm_head [248320 x 2048] 8-bit in 4 vocab slices, f32 logits, argmax."""
         torch, dh = self.torch, self.dh
@@ -466,6 +502,10 @@ def main():
     if on("dense"):
         res["dense"] = b.dense(steps, warmup)
         log(f"[dense] {res['dense']['TFLOP_s']:.1f} TFLOP/s")
+    if on("attention"):
+        res["attention"] = b.attention(steps, warmup)
+        for name, r in res["attention"].items():
+            log(f"[attention] {name}: {r['ms'] * 1e3:.1f} us, {r['TFLOP_s']:.1f} TFLOP/s, KV {r['kv_GB_s']:.0f} GB/s")
     if "load" in wls:
         res["load"] = b.load()
         log(f"[load] {res['load']['GB_s']:.1f} GB/s ({res['load']['bytes'] / 1e6:.0f} MB in {res['load']['ms']:.1f} ms)")
@@ -498,6 +538,8 @@ def main():
                     "bytes_per_launch": dom[1]["bytes"]}
     else:
         k, v = next(iter(res.items()))
+        if k == "attention":
+            v = v["chunk2048_pos30720"]
         head = {"metric": metric_name(), "value": v.get("GB_s") or v.get("TFLOP_s"),
                 "unit": "GB/s" if "GB_s" in v else "TFLOP/s", "ms_per_step": v.get("ms_per_step", v.get("ms")),
                 "dtype": "bf16" if k in ("prefill", "prefill5", "dense") else "f32", "config": {"workload": k}}

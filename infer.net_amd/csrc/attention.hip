@@ -25,6 +25,8 @@
 // GPU; each partition writes (max, sum) and its unnormalized 256 values and a combine
 // kernel merges them (graph_attention_combine). With one partition the block finishes
 // the output itself.
+#include <algorithm>
+
 #include "dih_device.h"
 #include "dih_internal.h"
 
@@ -34,7 +36,6 @@ namespace {
 constexpr int kHeads = 16, kKvHeads = 2, kDim = 256, kGroup = kHeads / kKvHeads;
 constexpr int kTok = 16;               // query tokens per block (128 rows)
 constexpr int kKeys = 32;              // keys per tile
-constexpr int kKsStride = kDim + 8;    // bf16 per key row in LDS: 528 B, 16 B aligned
 constexpr int kVtStride = kKeys + 4;   // bf16 per transposed value row: 72 B, conflict-free reads
 constexpr float kLog2eOver16 = 1.4426950408889634f / 16.f;
 
@@ -80,8 +81,60 @@ DIH_DEV void store_out4(const AttnParams &P, int tok, int head, int d0, const fl
     }
 }
 
+// Keys reach LDS by direct global->LDS copies (no registers), double-buffered: key row kl
+// (512 B) holds its 16-byte piece c at slot c ^ (kl & 15), which makes the MFMA operand
+// reads (16 lanes = 16 keys, one piece each) conflict-free. Wave w copies rows 8w..8w+7, two
+// rows per instruction. Key indices past the partition end are clamped to its last key
+// (finite data; those keys are masked).
+DIH_DEV void issue_keys(const uint16_t *kbase, uint16_t *ksbuf, int kb, int kend, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int kl = 8 * wave + 2 * i + (lane >> 5);
+        const int c = (lane & 31) ^ (kl & 15);
+        const uint32_t key = (uint32_t)min(kb + kl, kend - 1);
+        // 32-bit element offset from the wave-uniform base (the cache is below 2^31 elements)
+        const uint32_t off = key * (uint32_t)(kKvHeads * kDim) + 8u * (uint32_t)c;
+        to_lds<16>(kbase + off, ksbuf + (8 * wave + 2 * i) * kDim);
+    }
+}
+
+// Values reach LDS the same way, untransposed (raw rows of 512 B, piece c at slot
+// c ^ (kl & 15)), into one buffer that is consumed by the transpose below before the next
+// tile's copies are issued.
+DIH_DEV void issue_values(const uint16_t *vbase, uint16_t *vraw, int kb, int kend, int wave, int lane) {
+    issue_keys(vbase, vraw, kb, kend, wave, lane);
+}
+
+DIH_DEV void store_vt_pair(uint16_t *vt, int d, int vq, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    // each word holds dims d (low half) and d+1 (high half) of one key
+    uint2 lo, hi;
+    lo.x = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+    lo.y = __builtin_amdgcn_perm(w3, w2, 0x05040100u);
+    hi.x = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+    hi.y = __builtin_amdgcn_perm(w3, w2, 0x07060302u);
+    *reinterpret_cast<uint2 *>(vt + d * kVtStride + 4 * vq) = lo;
+    *reinterpret_cast<uint2 *>(vt + (d + 1) * kVtStride + 4 * vq) = hi;
+}
+
+// Transpose: thread t reads the 8 dims of chunk t/8 of keys 4*(t%8) + i from the raw rows
+// and writes dim d of those four keys as one 8-byte word of row d.
+DIH_DEV void transpose_values(const uint16_t *vraw, uint16_t *vt, int vq, int vc) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int kl = 4 * vq + i;
+        v[i] = *reinterpret_cast<const uint4 *>(vraw + kl * kDim + 8 * (vc ^ (kl & 15)));
+    }
+    const int d = 8 * vc;
+    store_vt_pair(vt, d, vq, v[0].x, v[1].x, v[2].x, v[3].x);
+    store_vt_pair(vt, d + 2, vq, v[0].y, v[1].y, v[2].y, v[3].y);
+    store_vt_pair(vt, d + 4, vq, v[0].z, v[1].z, v[2].z, v[3].z);
+    store_vt_pair(vt, d + 6, vq, v[0].w, v[1].w, v[2].w, v[3].w);
+}
+
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
-    __shared__ __align__(16) uint16_t ks[kKeys * kKsStride];
+    __shared__ __align__(16) uint16_t ks[2][kKeys * kDim];
+    __shared__ __align__(16) uint16_t vraw[kKeys * kDim];
     __shared__ __align__(16) uint16_t vt[kDim * kVtStride];
 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, r = lane & 31, h = lane >> 5;
@@ -125,47 +178,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
         }
     }
 
-    // ---- tile loads. Keys: thread t copies 16 B (8 dims) of keys t/32 + 8i. Values: thread
-    // t loads 8 dims (chunk t/8) of the 4 keys 4*(t%8) + i and writes them transposed.
-    // Key indices past the partition end are clamped to its last key (finite data; those
-    // keys are masked).
+    // ---- tiles are copied one compute phase ahead
     const uint16_t *kbase = P.keys + kh * kDim, *vbase = P.values + kh * kDim;
-    const int kc = t & 31, kr = t >> 5;
     const int vq = t & 7, vc = t >> 3;
-    uint4 kreg[4], vreg[4];
-    auto load_tile = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = min(kb + kr + 8 * i, kend - 1);
-            kreg[i] = *reinterpret_cast<const uint4 *>(kbase + (size_t)key * (kKvHeads * kDim) + 8 * kc);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = min(kb + 4 * vq + i, kend - 1);
-            vreg[i] = *reinterpret_cast<const uint4 *>(vbase + (size_t)key * (kKvHeads * kDim) + 8 * vc);
-        }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            *reinterpret_cast<uint4 *>(ks + (kr + 8 * i) * kKsStride + 8 * kc) = kreg[i];
-        const uint32_t w0[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};
-        const uint32_t w1[4] = {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w};
-        const uint32_t w2[4] = {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w};
-        const uint32_t w3[4] = {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w};
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            // word w of each key holds dims 2w (low half) and 2w+1 (high half)
-            uint2 lo, hi;
-            lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
-            lo.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u);
-            hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
-            hi.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u);
-            *reinterpret_cast<uint2 *>(vt + (8 * vc + 2 * w) * kVtStride + 4 * vq) = lo;
-            *reinterpret_cast<uint2 *>(vt + (8 * vc + 2 * w + 1) * kVtStride + 4 * vq) = hi;
-        }
-    };
-
     float m_run = -INFINITY, l_run = 0.f;
     dih_f32x16 acc[8];
 #pragma unroll
@@ -173,12 +188,18 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
 #pragma unroll
         for (int k = 0; k < 16; k++) acc[i][k] = 0.f;
 
-    load_tile(kstart);
-    for (int kb = kstart; kb < kend; kb += kKeys) {
-        __syncthreads();          // the previous tile's LDS reads are done
-        store_tile();
-        __syncthreads();
-        if (kb + kKeys < kend) load_tile(kb + kKeys);
+    issue_keys(kbase, ks[0], kstart, kend, wave, lane);
+    issue_values(vbase, vraw, kstart, kend, wave, lane);
+    int buf = 0;
+    for (int kb = kstart; kb < kend; kb += kKeys, buf ^= 1) {
+        wait_vm<0>();             // this thread's copies have landed
+        __syncthreads();          // every thread's copies are in LDS; the previous tile's reads are done
+        transpose_values(vraw, vt, vq, vc);
+        __syncthreads();          // vt complete, vraw consumed
+        if (kb + kKeys < kend) {
+            issue_keys(kbase, ks[buf ^ 1], kb + kKeys, kend, wave, lane);
+            issue_values(vbase, vraw, kb + kKeys, kend, wave, lane);
+        }
         if (!wave_ok || kb > wave_last) continue;
 
         // ---- S^T = K Q^T: s[k] is key kb + 8(k/4) + 4h + k%4 of row r
@@ -187,40 +208,53 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
         for (int k = 0; k < 16; k++) s[k] = 0.f;
 #pragma unroll
         for (int st = 0; st < 16; st++) {
-            const dih_bf16x8 a = *reinterpret_cast<const dih_bf16x8 *>(ks + r * kKsStride + 16 * st + 8 * h);
+            const dih_bf16x8 a = *reinterpret_cast<const dih_bf16x8 *>(ks[buf] + r * kDim + 8 * ((2 * st + h) ^ (r & 15)));
             s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[st], s, 0, 0, 0);
         }
-        // ---- online softmax for row r
+        // ---- online softmax for row r. Tiles every row of the wave sees whole (all but the
+        // diagonal and partition-end tiles) skip the mask. Scores stay raw here; the log2
+        // scale enters the exponent's FMA.
+        const bool full = kb + kKeys - 1 <= P.position + wtok0 && kb + kKeys <= kend;
         float mx = -INFINITY;
+        if (full) {
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int key = kb + 8 * (k >> 2) + 4 * h + (k & 3);
-            const bool ok = key <= my_last && key < kend;
-            s[k] = ok ? s[k] * kLog2eOver16 : -INFINITY;
-            mx = fmaxf(mx, s[k]);
+            for (int k = 0; k < 16; k++) mx = fmaxf(mx, s[k]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const int key = kb + 8 * (k >> 2) + 4 * h + (k & 3);
+                s[k] = key <= my_last && key < kend ? s[k] : -INFINITY;
+                mx = fmaxf(mx, s[k]);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
+        const float m_new = fmaxf(m_run, mx * kLog2eOver16);
         const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;   // all keys masked so far: p = 0
         float psum = 0.f;
         uint32_t pw[8];
 #pragma unroll
         for (int k = 0; k < 16; k += 2) {
-            const float p0 = s[k] == -INFINITY ? 0.f : exp2f(s[k] - m_new);
-            const float p1 = s[k + 1] == -INFINITY ? 0.f : exp2f(s[k + 1] - m_new);
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k], kLog2eOver16, -m_use));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[k + 1], kLog2eOver16, -m_use));
             psum += p0 + p1;
             pw[k >> 1] = pack_bf16x2(p0, p1);
         }
         psum += __shfl_xor(psum, 32, 64);
         l_run = l_run * alpha + psum;
         m_run = m_new;
+        // rescale only when some row's maximum moved (alpha == 1 exactly otherwise)
+        if (__ballot(alpha != 1.f)) {
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int k = 0; k < 16; k++) acc[dt][k] *= alpha;
+        }
         const dih_bf16x8 pb0 = __builtin_bit_cast(dih_bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
         const dih_bf16x8 pb1 = __builtin_bit_cast(dih_bf16x8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
         // ---- O^T = O^T * alpha + V^T P^T: acc[dt][k] is dim 32dt + 8(k/4) + 4h + k%4 of row r
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) acc[dt][k] *= alpha;
             const uint16_t *vrow = vt + (32 * dt + r) * kVtStride + 4 * h;
             const uint2 a0 = *reinterpret_cast<const uint2 *>(vrow);
             const uint2 a1 = *reinterpret_cast<const uint2 *>(vrow + 8);
@@ -257,28 +291,52 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
     }
 }
 
-// One block per (token, head), one thread per dim: merge the partitions that hold keys
-// of this token (graph_attention_combine, gpu_graph.mm:199-213).
+// One wave per (token, head), four dims per lane: merge the partitions that hold keys of
+// this token (graph_attention_combine, gpu_graph.mm:199-213). Each lane computes the
+// weight exp(m_p - M) of one partition of a 64-partition chunk; the chunk's partial rows
+// are then read eight at a time (independent loads) with the weights broadcast by lane.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
-    const int th = blockIdx.x, tok = th / kHeads, head = th - tok * kHeads, d = threadIdx.x;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int th = blockIdx.x * 4 + wv;            // tok * 16 + head
+    if (th >= P.tokens * kHeads) return;
+    const int tok = th / kHeads, head = th - tok * kHeads;
     const int np = (P.position + tok) / P.partition + 1;
-    const size_t pi = ((size_t)tok * kHeads + head) * P.nparts;
+    const size_t pi = (size_t)th * P.nparts;
+    const float2 *st = P.pstat + pi;
     float m = -INFINITY;
-    for (int p = 0; p < np; p++) m = fmaxf(m, P.pstat[pi + p].x);
-    float total = 0.f, acc = 0.f;
-    for (int p = 0; p < np; p++) {
-        const float2 st = P.pstat[pi + p];
-        const float w = exp2f(st.x - m);
-        total += w * st.y;
-        acc += w * P.pacc[(pi + p) * kDim + d];
+    for (int p = lane; p < np; p += 64) m = fmaxf(m, st[p].x);
+    m = wave_max(m);
+    float total = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 *pa = reinterpret_cast<const float4 *>(P.pacc + pi * kDim) + lane;
+    for (int c0 = 0; c0 < np; c0 += 64) {
+        const int n = min(64, np - c0);
+        float w = 0.f;
+        if (lane < n) {
+            const float2 v = st[c0 + lane];
+            w = exp2f(v.x - m);
+            total += w * v.y;
+        }
+        int p = 0;
+        for (; p + 8 <= n; p += 8) {
+            float4 a[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) a[j] = pa[(size_t)(c0 + p + j) * (kDim / 4)];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float wj = __shfl(w, p + j, 64);
+                acc.x += wj * a[j].x; acc.y += wj * a[j].y; acc.z += wj * a[j].z; acc.w += wj * a[j].w;
+            }
+        }
+        for (; p < n; p++) {
+            const float4 a = pa[(size_t)(c0 + p) * (kDim / 4)];
+            const float wj = __shfl(w, p, 64);
+            acc.x += wj * a.x; acc.y += wj * a.y; acc.z += wj * a.z; acc.w += wj * a.w;
+        }
     }
-    const float v = acc / total * sigmoid_f(load_any(P.gate, P.gate_bf16,
-                                                     (size_t)tok * (kHeads * 2 * kDim) + head * 2 * kDim + kDim + d));
-    const size_t oi = (size_t)tok * (kHeads * kDim) + head * kDim + d;
-    if (P.out_bf16)
-        static_cast<uint16_t *>(P.out)[oi] = f32_to_bf16(v);
-    else
-        static_cast<float *>(P.out)[oi] = v;
+    total = wave_sum(total);
+    const float a4[4] = {acc.x, acc.y, acc.z, acc.w};
+    store_out4(P, tok, head, 4 * lane, a4, 1.f / total);
 }
 
 }  // namespace
@@ -286,12 +344,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
 int attention_partition(int position, int tokens, int requested) {
     if (requested > 0) return requested;
     const int ntiles = (tokens + kTok - 1) / kTok;
-    const int items = ntiles * kKvHeads;
     const int keys = position + tokens;
-    // Enough (tile, head, partition) items for about two blocks per CU of a 256-CU part.
-    constexpr int kTarget = 512;
-    if (items >= kTarget) return ((keys + kKeys - 1) / kKeys) * kKeys;
-    const int parts = (kTarget + items - 1) / items;
+    if (ntiles == 1) {
+        // decode / short chunks: the key stream is latency-bound; about 128 partitions per
+        // KV head of at least 128 keys (measured best at 8K and 32K positions)
+        const int part = (((keys + 127) / 128) + 127) / 128 * 128;
+        return part < 128 ? 128 : part;
+    }
+    // (tile, KV head, partition) items: two blocks per CU of the 256-CU part, more when the
+    // keys are long (the partial results stay small against the key stream then)
+    const int items = ntiles * kKvHeads;
+    const int target = 512 * std::min(4, std::max(1, keys / 8192));
+    if (items >= target) return ((keys + kKeys - 1) / kKeys) * kKeys;
+    const int parts = (target + items - 1) / items;
     int part = (keys + parts - 1) / parts;
     part = ((part + 255) / 256) * 256;
     return part < 256 ? 256 : part;
@@ -312,10 +377,12 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
         return false;
     }
     const int per = ((P.ntiles * P.nparts + 3) / 4) * 4;
+    prof_stage("attention");
     DIH_LAUNCH(attn_kernel, dim3(2 * per), dim3(256), 0, s, P);
     if (!hip_ok(hipGetLastError(), error, capacity, "attention launch")) return false;
     if (P.nparts > 1) {
-        DIH_LAUNCH(attn_combine_kernel, dim3(a.tokens * kHeads), dim3(256), 0, s, P);
+        prof_stage("attention_combine");
+        DIH_LAUNCH(attn_combine_kernel, dim3((a.tokens * kHeads + 3) / 4), dim3(256), 0, s, P);
         if (!hip_ok(hipGetLastError(), error, capacity, "attention combine launch")) return false;
     }
     return true;

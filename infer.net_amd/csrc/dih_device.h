@@ -253,3 +253,31 @@ DIH_DEV void load_x32(float *x, const void *base, int x_bf16, int offset) {
         }
     }
 }
+
+// ---- direct global->LDS copies and the waits around them
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+template <int SIZE>
+DIH_DEV void to_lds(const void *src, void *lds_wave_base) {
+    if constexpr (SIZE == 16)
+        __builtin_amdgcn_global_load_lds((gbl_void_t *)src, (lds_void_t *)lds_wave_base, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((gbl_void_t *)src, (lds_void_t *)lds_wave_base, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding)
+template <int N>
+DIH_DEV void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+// s_waitcnt lgkmcnt(0) leaving the other counters alone
+DIH_DEV void wait_lgkm0() { __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+// Workgroup barrier without a memory fence: __syncthreads() would also wait for every
+// outstanding copy (the fence counts LDS copies as pending stores). Callers first wait
+// for their own copies of the step with wait_vm; the "memory" clobber keeps the compiler
+// from moving LDS accesses across the barrier.
+DIH_DEV void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }

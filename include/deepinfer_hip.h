@@ -266,6 +266,26 @@ int dih_attention(void *context, const void *q, int q_dtype, const uint16_t *key
  * tokens * 16 * ceil((position + tokens) / partition) * 1032 bytes when above one. */
 int dih_attention_partition(int position, int tokens, int partition);
 
+/* Gated delta rule of a linear-attention (Gated DeltaNet) layer over a chunk of `tokens`
+ * tokens: p_delta (gpu_prefill.mm:540-551), i.e. the sequential prefill_delta
+ * (gpu_prefill.mm:177-191) below 64 tokens and the chunkwise prefill_delta_prepare /
+ * prefill_delta_apply (prefill_delta.mm:8-181) from 64 tokens on. For every token t, value
+ * head h (32) and value row r (128), with key head h/2:
+ *   S[h][r] *= decay[t][h];  c = (v - S[h][r].k) * beta[t][h];  S[h][r] += c k;
+ *   out[t][h*128+r] = S[h][r].q
+ * where the convolved row conv[t] [8192] holds q (16 x 128) at 0, k at 2048 and v
+ * (32 x 128) at 4096. Then the convolution history [3][8192] rolls forward over the raw
+ * projection rows raw[t] [8192] (gpu_prefill.mm:189-190).
+ *   state   f32 [32][128][128], read and updated in place
+ *   history f32 [3][8192], updated in place
+ *   conv, raw f32 [tokens][8192]; decay, beta f32 [tokens][32]; out f32 [tokens][4096]
+ *   path    0: the reference's choice; 1: sequential; 2: chunkwise (any token count)
+ * Device pointers; runs on `stream` (NULL: the context's stream). Returns 0, or -1 with a
+ * message when an argument is invalid (nothing is launched then). */
+int dih_delta_rule(void *context, float *state, float *history, const float *conv,
+                   const float *decay, const float *beta, const float *raw, float *out,
+                   int tokens, int path, void *stream, char *error, int capacity);
+
 /* Per-stage GPU timing (the reference's DEEPINFER_METAL_GPU_PROFILE per-dispatch
  * timestamps, gpu_graph.mm:329-338, as a runtime switch instead of getenv). While enabled,
  * every device-resident call records HIP events on its own stream between its kernels.

@@ -969,6 +969,36 @@ __attribute__((visibility("default"))) int dih_attention(void *ctx, const void *
     return ok ? 0 : -1;
 }
 
+__attribute__((visibility("default"))) int dih_delta_rule(void *ctx, float *state, float *history, const float *conv,
+                                                          const float *decay, const float *beta, const float *raw,
+                                                          float *out, int tokens, int path, void *stream,
+                                                          char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c || !state || !history || !conv || !decay || !beta || !raw || !out || tokens < 1 ||
+        tokens > (1 << 20) || path < 0 || path > 2) {
+        set_error(error, capacity, "Invalid delta rule arguments");
+        return -1;
+    }
+    DeltaArgs a;
+    a.conv = conv; a.decay = decay; a.beta = beta; a.raw = raw;
+    a.state = state; a.history = history; a.out = out; a.tokens = tokens;
+    // p_delta (gpu_prefill.mm:540-551): chunkwise from 64 tokens, sequential below
+    a.chunked = path == 0 ? tokens >= 64 : path == 2;
+    if (a.chunked) {
+        const size_t blocks = ((size_t)tokens + 31) / 32, tiles = blocks * 32;
+        a.w = static_cast<float *>(scratch(c, S_DW, tiles * 32 * 128 * 4, error, capacity));
+        a.u = static_cast<float *>(scratch(c, S_DU, tiles * 32 * 128 * 4, error, capacity));
+        a.causal = static_cast<float *>(scratch(c, S_DC, tiles * 32 * 32 * 4, error, capacity));
+        a.factors = static_cast<float *>(scratch(c, S_DF, tiles * 32 * 2 * 4, error, capacity));
+        if (!a.w || !a.u || !a.causal || !a.factors) return -1;
+    }
+    hipStream_t s = pick(c, stream);
+    ProfScope prof_scope(c);
+    bool ok = launch_delta_rule(a, s, error, capacity);
+    prof_mark(c, s, "delta");
+    return ok ? 0 : -1;
+}
+
 __attribute__((visibility("default"))) int dih_attention_partition(int position, int tokens, int partition) {
     if (tokens < 1 || position < 0 || partition < 0 || partition % 32 != 0) return -1;
     return attention_partition(position, tokens, partition);

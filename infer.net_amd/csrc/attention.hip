@@ -49,10 +49,6 @@ struct AttnParams {
     int position, tokens, partition, nparts, ntiles;
 };
 
-DIH_DEV float load_any(const void *p, int bf16, size_t i) {
-    return bf16 ? bf16_to_f32(static_cast<const uint16_t *>(p)[i]) : static_cast<const float *>(p)[i];
-}
-
 DIH_DEV float sigmoid_f(float g) { return 1.f / (1.f + __expf(-g)); }
 
 // Four consecutive output values of one row: out = acc * inv * sigmoid(gate).

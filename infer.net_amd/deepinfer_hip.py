@@ -84,7 +84,7 @@ EXPORTS = [
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
     "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm",
     "dih_moe_prefill_norm", "dih_dense", "dih_attention",
-    "dih_attention_partition", "dih_set_profiling",
+    "dih_attention_partition", "dih_delta_rule", "dih_set_profiling",
     "dih_profile_read", "dih_version",
     "dih_safetensors_open", "dih_safetensors_close", "dih_safetensors_count",
     "dih_safetensors_info", "dih_safetensors_get", "dih_safetensors_read",
@@ -138,6 +138,7 @@ def load():
         "dih_dense": ([P, P, I, P, P, I, P, E, I], I),
         "dih_attention": ([P, P, I, P, P, I, P, I, P, I, I, I, I, P, E, I], I),
         "dih_attention_partition": ([I, I, I], I),
+        "dih_delta_rule": ([P, P, P, P, P, P, P, P, I, I, P, E, I], I),
         "dih_set_profiling": ([P, I], I),
         "dih_profile_read": ([P, P, P, P, I], I),
         "dih_version": ([], ctypes.c_char_p),
@@ -559,6 +560,16 @@ def attention(dev, q, keys, values, gate, out, position, tokens, partition=0, q_
     _check(dev._lib.dih_attention(_ctx(dev), _dp(q), q_dtype, _dp(keys), _dp(values), cache_positions,
                                   _dp(gate), gate_dtype, _dp(out), out_dtype, position, tokens, partition,
                                   _stream(stream), err, _ERR), err, ArgumentError)
+
+
+def delta_rule(dev, state, history, conv, decay, beta, raw, out, tokens, path=0, stream=None) -> None:
+    """Gated delta rule over a chunk (dih_delta_rule; p_delta, gpu_prefill.mm:540-551).
+    path 0: chunkwise from 64 tokens, sequential below (the reference's choice); 1:
+    sequential; 2: chunkwise."""
+    err = _errbuf()
+    _check(dev._lib.dih_delta_rule(_ctx(dev), _dp(state), _dp(history), _dp(conv), _dp(decay), _dp(beta),
+                                   _dp(raw), _dp(out), tokens, path, _stream(stream), err, _ERR),
+           err, ArgumentError)
 
 
 def attention_partition(position, tokens, partition=0) -> int:

@@ -379,6 +379,50 @@ def attention_f64(q, keys, values, gate_raw, position, bf16_operands=True, parti
     return (out / (1.0 + np.exp(-gate))).reshape(T, ATT_HEADS * D)
 
 
+# ---------------------------------------------------------------- gated delta rule (numpy)
+# Linear-attention (Gated DeltaNet) layer geometry as the reference hard-codes it: the
+# convolved projection row [8192] holds q (16 key heads x 128) at 0, k (16 x 128) at 2048
+# and v (32 value heads x 128) at 4096; value head h reads key head h/2; the state is
+# [32 heads][128 value rows][128 key dims] f32 (gpu_prefill.mm:177-191).
+DELTA_HEADS, DELTA_KEY_HEADS, DELTA_DIM, DELTA_ROW = 32, 16, 128, 8192
+
+
+def delta_rule_f64(state, conv, decay, beta, tokens):
+    """The gated delta rule, token by token in float64 (prefill_delta_checks.mm:33-37, the
+    recurrence of prefill_delta gpu_prefill.mm:181-187). For every token t and value row
+    (head h, row r; key head h/2):
+        S[h,r,:] *= a[t,h]
+        c = (v[t,h,r] - S[h,r,:].k[t]) * b[t,h]
+        S[h,r,:] += k[t] * c
+        out[t, h*128+r] = S[h,r,:].q[t]
+    state [32,128,128] (not modified), conv [>=tokens, 8192], decay/beta [>=tokens, 32].
+    Returns (out [tokens, 4096], state after the chunk), float64."""
+    S = np.array(state, dtype=np.float64).reshape(DELTA_HEADS, DELTA_DIM, DELTA_DIM)
+    conv = np.asarray(conv, dtype=np.float64)
+    a = np.asarray(decay, dtype=np.float64)
+    b = np.asarray(beta, dtype=np.float64)
+    kh = np.arange(DELTA_HEADS) // 2
+    out = np.zeros((tokens, DELTA_HEADS * DELTA_DIM))
+    for t in range(tokens):
+        q = conv[t, :2048].reshape(DELTA_KEY_HEADS, DELTA_DIM)[kh]          # [32,128]
+        k = conv[t, 2048:4096].reshape(DELTA_KEY_HEADS, DELTA_DIM)[kh]
+        v = conv[t, 4096:8192].reshape(DELTA_HEADS, DELTA_DIM)
+        S *= a[t, :, None, None]
+        pred = np.einsum("hrd,hd->hr", S, k)
+        corr = (v - pred) * b[t, :, None]
+        S += corr[:, :, None] * k[:, None, :]
+        out[t] = np.einsum("hrd,hd->hr", S, q).reshape(-1)
+    return out, S
+
+
+def delta_history(history, raw, tokens):
+    """The convolution history after a chunk (gpu_prefill.mm:189-190): row j of the new
+    [3, 8192] history is old row j+tokens when j+tokens < 3, else raw row j+tokens-3."""
+    h = np.asarray(history)
+    r = np.asarray(raw)
+    return np.stack([h[j + tokens] if j + tokens < 3 else r[j + tokens - 3] for j in range(3)])
+
+
 def cpu_qmv(m: QMatrix, x, experts=None, batched=False, threads=1) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     count = 1 if experts is None else len(experts)

@@ -419,3 +419,91 @@ def test_attention_causal_mask():
     moved = orc.attention_f64(q, k2, v2, g, 20)
     assert np.array_equal(base[:2], moved[:2])
     assert np.all(np.max(np.abs(base[2:] - moved[2:]), axis=1) > 1e-3)
+
+
+# ---------------------------------------------------------------- gated delta rule
+
+def _delta_inputs(T, seed=4, unit_k=True):
+    rng = np.random.default_rng(seed)
+    conv = rng.normal(size=(T, 8192)).astype(np.float32) * 0.3
+    if unit_k:
+        k = conv[:, 2048:4096].reshape(T, 16, 128).astype(np.float64)
+        k /= np.linalg.norm(k, axis=2, keepdims=True)
+        conv[:, 2048:4096] = k.reshape(T, 2048)
+    state = (rng.normal(size=(32, 128, 128)) * 0.01).astype(np.float32)
+    a = rng.uniform(0.5, 1.0, size=(T, 32)).astype(np.float32)
+    b = rng.uniform(0.0, 1.0, size=(T, 32)).astype(np.float32)
+    return state, conv, a, b
+
+
+def test_delta_rule_closed_forms():
+    """a = 1, b = 0 leaves the state alone and reads it out: out = S0 q. a = 0, b = 1 with
+    unit keys forgets everything: S_t = v_t k_t^T, so out_t = v_t (k_t . q_t)."""
+    state, conv, a, b = _delta_inputs(5)
+    out, S = orc.delta_rule_f64(state, conv, np.ones_like(a), np.zeros_like(b), 5)
+    assert np.array_equal(S, state.astype(np.float64))
+    q = conv[:, :2048].reshape(5, 16, 128).astype(np.float64)[:, np.arange(32) // 2]
+    want = np.einsum("hrd,thd->thr", state.astype(np.float64), q).reshape(5, 4096)
+    assert np.allclose(out, want, rtol=1e-12, atol=1e-15)
+    out, S = orc.delta_rule_f64(state, conv, np.zeros_like(a), np.ones_like(b), 5)
+    k = conv[:, 2048:4096].reshape(5, 16, 128).astype(np.float64)[:, np.arange(32) // 2]
+    v = conv[:, 4096:].reshape(5, 32, 128).astype(np.float64)
+    assert np.allclose(out, (v * np.einsum("thd,thd->th", k, q)[:, :, None]).reshape(5, 4096), rtol=1e-12,
+                       atol=1e-14)
+    assert np.allclose(S, v[-1][:, :, None] * k[-1][:, None, :], rtol=1e-12, atol=1e-15)
+
+
+def test_delta_rule_writes_the_value():
+    """The delta rule's defining property: with b = 1 the updated state maps k_t to
+    a*S_prev*k_t*(1 - |k_t|^2) + v_t*|k_t|^2, i.e. to v_t exactly for a unit key, whatever
+    it held before and whatever the decay."""
+    state, conv, a, b = _delta_inputs(3, seed=6)
+    for t in range(1, 4):
+        bb = b.copy()
+        bb[t - 1] = 1.0
+        _, S0 = orc.delta_rule_f64(state, conv, a, bb, t - 1)
+        _, S = orc.delta_rule_f64(state, conv, a, bb, t)
+        k = conv[t - 1, 2048:4096].reshape(16, 128).astype(np.float64)[np.arange(32) // 2]
+        v = conv[t - 1, 4096:].reshape(32, 128).astype(np.float64)
+        kk = np.sum(k * k, axis=1)[:, None]
+        prev = a[t - 1][:, None].astype(np.float64) * np.einsum("hrd,hd->hr", S0, k)
+        assert np.allclose(np.einsum("hrd,hd->hr", S, k), prev * (1 - kk) + v * kk, rtol=1e-11, atol=1e-13)
+        assert np.max(np.abs(kk - 1)) < 1e-6 and np.allclose(np.einsum("hrd,hd->hr", S, k), v, atol=1e-5)
+
+
+def test_delta_rule_brute_force_rows():
+    """Pure-Python loops over a few rows (independent of the vectorized head mapping)."""
+    T = 4
+    state, conv, a, b = _delta_inputs(T, seed=7, unit_k=False)
+    out, S = orc.delta_rule_f64(state, conv, a, b, T)
+    for head, row in ((0, 0), (5, 77), (31, 127)):
+        s = [float(x) for x in state[head, row]]
+        kh = head // 2
+        for t in range(T):
+            s = [x * float(a[t, head]) for x in s]
+            k = [float(conv[t, 2048 + kh * 128 + d]) for d in range(128)]
+            q = [float(conv[t, kh * 128 + d]) for d in range(128)]
+            pred = sum(x * y for x, y in zip(s, k))
+            c = (float(conv[t, 4096 + head * 128 + row]) - pred) * float(b[t, head])
+            s = [x + y * c for x, y in zip(s, k)]
+            assert abs(out[t, head * 128 + row] - sum(x * y for x, y in zip(s, q))) < 1e-12
+        assert np.allclose(S[head, row], s, rtol=0, atol=1e-14)
+
+
+def test_delta_rule_chunk_composition():
+    """Two calls that carry the state equal one call over the whole sequence."""
+    T = 9
+    state, conv, a, b = _delta_inputs(T, seed=8)
+    out, S = orc.delta_rule_f64(state, conv, a, b, T)
+    o1, S1 = orc.delta_rule_f64(state, conv, a, b, 4)
+    o2, S2 = orc.delta_rule_f64(S1, conv[4:], a[4:], b[4:], 5)
+    assert np.allclose(np.concatenate([o1, o2]), out, rtol=1e-12, atol=1e-15)
+    assert np.allclose(S2, S, rtol=1e-12, atol=1e-15)
+
+
+def test_delta_history_roll():
+    hist = np.arange(3 * 8)[:, None].repeat(2, 1).reshape(3, 16)[:, :8].astype(np.float32)
+    raw = 100 + np.arange(5 * 8).reshape(5, 8).astype(np.float32)
+    assert np.array_equal(orc.delta_history(hist, raw, 1), np.stack([hist[1], hist[2], raw[0]]))
+    assert np.array_equal(orc.delta_history(hist, raw, 2), np.stack([hist[2], raw[0], raw[1]]))
+    assert np.array_equal(orc.delta_history(hist, raw, 5), raw[2:5])

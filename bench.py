@@ -352,6 +352,43 @@ class Bench:
             del keys, vals, q, raw, y
         return out
 
+    def delta(self, steps, warmup):
+        """Gated delta rule of one linear-attention layer (p_delta, gpu_prefill.mm:540-551):
+        32 value heads x 128 rows x 128 key dims of f32 state, for a 2048-token chunk
+        (chunkwise), a 63-token chunk (sequential, the longest below the switch) and one
+        decode token. FLOPs count the recurrence's own work, 4 x 2 x 128 x 128 per head and
+        token (decay, prediction, update, readout)."""
+        torch, dh = self.torch, self.dh
+        out = {}
+        cases = [("chunk2048", 2048, 0), ("chunk2048_sequential", 2048, 1), ("chunk63", 63, 0),
+                 ("chunk63_chunkwise", 63, 2), ("decode1", 1, 0)]
+        if getattr(self.args, "delta_sweep", False):
+            cases += [(f"chunk{T}_{p}", T, i) for T in (128, 192, 256, 384, 512, 1024)
+                      for i, p in ((1, "sequential"), (2, "chunkwise"))]
+        for name, T, path in cases:
+            g = torch.Generator(device="cuda").manual_seed(7)
+            conv = torch.randn((T, 8192), device="cuda", generator=g) * 0.1
+            k = conv[:, 2048:4096].view(T, 16, 128)
+            k /= k.norm(dim=2, keepdim=True)
+            a = torch.rand((T, 32), device="cuda", generator=g) * 0.1 + 0.9
+            b = torch.rand((T, 32), device="cuda", generator=g)
+            raw = torch.randn((T, 8192), device="cuda", generator=g)
+            state = torch.randn((32, 128, 128), device="cuda", generator=g) * 0.01
+            hist = torch.zeros((3, 8192), device="cuda")
+            y = torch.zeros((T, 4096), device="cuda")
+
+            def step(i, conv=conv, a=a, b=b, raw=raw, state=state, hist=hist, y=y, T=T, path=path):
+                dh.delta_rule(self.dev, state, hist, conv, a, b, raw, y, T, path=path)
+
+            n = max(8, steps // 8) if T > 1 else max(16, steps)
+            ms, prof = self.timed_graph(step, n, min(warmup, 3))
+            flops = 8.0 * 128 * 128 * 32 * T
+            stages = {k2: {"avg_us": v[0] / max(v[1], 1) * 1e3, "launches": v[1]} for k2, v in prof.items()}
+            out[name] = {"tokens": T, "path": ["auto", "sequential", "chunkwise"][path], "ms": ms, "us_per_token": ms * 1e3 / T, "GFLOP": flops / 1e9,
+                         "TFLOP_s": flops / (ms * 1e-3) / 1e12, "stages": stages}
+            del conv, a, b, raw, state, hist, y
+        return out
+
     def lm_head(self, steps, warmup, copies=2):
         """Config 5b: lm_head [248320 x 2048] 8-bit in 4 vocab slices, f32 logits, argmax."""
         torch, dh = self.torch, self.dh
@@ -472,6 +509,7 @@ def main():
     ap.add_argument("--workload", default="all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--delta-sweep", action="store_true", help="delta: both paths at 128..1024 tokens")
     ap.add_argument("--layers", type=int, default=24,
                     help="decode: rotating layer copies (24 x 855 MB keeps every step's weights out of the 256 MB MALL)")
     args = ap.parse_args()
@@ -506,6 +544,10 @@ def main():
         res["attention"] = b.attention(steps, warmup)
         for name, r in res["attention"].items():
             log(f"[attention] {name}: {r['ms'] * 1e3:.1f} us, {r['TFLOP_s']:.1f} TFLOP/s, KV {r['kv_GB_s']:.0f} GB/s")
+    if on("delta"):
+        res["delta"] = b.delta(steps, warmup)
+        for name, r in res["delta"].items():
+            log(f"[delta] {name}: {r['ms'] * 1e3:.1f} us ({r['us_per_token']:.2f} us/token), {r['TFLOP_s']:.2f} TFLOP/s")
     if "load" in wls:
         res["load"] = b.load()
         log(f"[load] {res['load']['GB_s']:.1f} GB/s ({res['load']['bytes'] / 1e6:.0f} MB in {res['load']['ms']:.1f} ms)")
@@ -540,6 +582,8 @@ def main():
         k, v = next(iter(res.items()))
         if k == "attention":
             v = v["chunk2048_pos30720"]
+        elif k == "delta":
+            v = v["chunk2048"]
         head = {"metric": metric_name(), "value": v.get("GB_s") or v.get("TFLOP_s"),
                 "unit": "GB/s" if "GB_s" in v else "TFLOP/s", "ms_per_step": v.get("ms_per_step", v.get("ms")),
                 "dtype": "bf16" if k in ("prefill", "prefill5", "dense") else "f32", "config": {"workload": k}}

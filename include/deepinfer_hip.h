@@ -268,8 +268,9 @@ int dih_attention_partition(int position, int tokens, int partition);
 
 /* Gated delta rule of a linear-attention (Gated DeltaNet) layer over a chunk of `tokens`
  * tokens: p_delta (gpu_prefill.mm:540-551), i.e. the sequential prefill_delta
- * (gpu_prefill.mm:177-191) below 64 tokens and the chunkwise prefill_delta_prepare /
- * prefill_delta_apply (prefill_delta.mm:8-181) from 64 tokens on. For every token t, value
+ * (gpu_prefill.mm:177-191) or the chunkwise prefill_delta_prepare / prefill_delta_apply
+ * (prefill_delta.mm:8-181); the library switches to the chunkwise form at 224 tokens (the
+ * reference at 64), where the two cost the same on MI355X. For every token t, value
  * head h (32) and value row r (128), with key head h/2:
  *   S[h][r] *= decay[t][h];  c = (v - S[h][r].k) * beta[t][h];  S[h][r] += c k;
  *   out[t][h*128+r] = S[h][r].q
@@ -279,7 +280,7 @@ int dih_attention_partition(int position, int tokens, int partition);
  *   state   f32 [32][128][128], read and updated in place
  *   history f32 [3][8192], updated in place
  *   conv, raw f32 [tokens][8192]; decay, beta f32 [tokens][32]; out f32 [tokens][4096]
- *   path    0: the reference's choice; 1: sequential; 2: chunkwise (any token count)
+ *   path    0: the library's choice; 1: sequential; 2: chunkwise (any token count)
  * Device pointers; runs on `stream` (NULL: the context's stream). Returns 0, or -1 with a
  * message when an argument is invalid (nothing is launched then). */
 int dih_delta_rule(void *context, float *state, float *history, const float *conv,

@@ -982,8 +982,11 @@ __attribute__((visibility("default"))) int dih_delta_rule(void *ctx, float *stat
     DeltaArgs a;
     a.conv = conv; a.decay = decay; a.beta = beta; a.raw = raw;
     a.state = state; a.history = history; a.out = out; a.tokens = tokens;
-    // p_delta (gpu_prefill.mm:540-551): chunkwise from 64 tokens, sequential below
-    a.chunked = path == 0 ? tokens >= 64 : path == 2;
+    // p_delta (gpu_prefill.mm:540-551) switches to the chunkwise form at 64 tokens; here the
+    // switch sits where the two measured equal on MI355X (sequential 55 us vs chunkwise 57 us
+    // at 192 tokens, 71 vs 68 us at 256)
+    constexpr int kChunkwiseFrom = 224;
+    a.chunked = path == 0 ? tokens >= kChunkwiseFrom : path == 2;
     if (a.chunked) {
         const size_t blocks = ((size_t)tokens + 31) / 32, tiles = blocks * 32;
         a.w = static_cast<float *>(scratch(c, S_DW, tiles * 32 * 128 * 4, error, capacity));

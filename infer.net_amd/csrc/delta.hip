@@ -25,8 +25,6 @@ namespace {
 
 constexpr int kVHeads = 32, kDim = 128, kBlk = 32, kRowLen = 8192;
 constexpr int kQ = 0, kK = 2048, kV = 4096;
-constexpr int kPad = kDim + 2;   // f32 row stride of [32][128] LDS tiles: two lanes halves hit disjoint banks
-constexpr int kSq = kBlk + 1;    // f32 row stride of [32][32] LDS tiles
 
 struct DeltaParams {
     const float *conv, *decay, *beta, *raw;
@@ -34,6 +32,18 @@ struct DeltaParams {
     float *w, *u, *causal, *factors;   // chunkwise scratch, indexed by tile = block * 32 + head
     int tokens, nblocks;
 };
+
+// (native vectors, not HIP's float4: copies of that struct go through memory, and such a
+// copy live across the loop is promoted to LDS)
+typedef dih_f32x4 f4;
+
+DIH_DEV f4 ld4(const float *p) { return *reinterpret_cast<const f4 *>(p); }
+DIH_DEV void st4(float *p, f4 v) { *reinterpret_cast<f4 *>(p) = v; }
+
+DIH_DEV f4 mask4(f4 v, bool keep) {
+    const f4 z = {0.f, 0.f, 0.f, 0.f};
+    return keep ? v : z;
+}
 
 DIH_DEV dih_f32x16 mfma_f32(float a, float b, dih_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -53,50 +63,148 @@ DIH_DEV void roll_history(const DeltaParams &P, int d) {
     for (int j = 0; j < 3; j++) P.history[j * kRowLen + d] = next[j];
 }
 
-// ---- sequential: one wave per value row, two key dims per lane (prefill_delta).
+// ---- sequential (prefill_delta): 16 lanes per value row, eight key dims per lane, a block
+// of four waves = 16 rows of one head. Token operands (keys and queries of the head's key
+// head, the block's 16 values, decay, beta) are staged through LDS 32 tokens at a time,
+// double-buffered: the next 32 tokens' global loads are in flight while the current ones
+// run, and each token's operands are read from LDS one token ahead.
+constexpr int kSeqChunk = 32;
+
+struct SeqStage {
+    float k[kSeqChunk * kDim], q[kSeqChunk * kDim], v[kSeqChunk * 16], a[kSeqChunk], b[kSeqChunk];
+};
+
+struct SeqRegs {
+    float4 k0, k1, k2, k3, q0, q1, q2, q3;
+    float v0, v1, ab;
+};
+
+// Thread t loads float4 j of keys / queries at flat index 4*(t + 256 j) of the chunk's
+// [32][128], values (token, row) = (t + 256 j) / 16, % 16, and decay (t < 32) or beta
+// (32 <= t < 64) of token t % 32. Tokens past the chunk end load token `last`.
+DIH_DEV float4 seq_row4(const DeltaParams &P, int t0, int last, int j, int tid, int off) {
+    const int i = 4 * (tid + 256 * j), t = min(t0 + (i >> 7), last), d = i & (kDim - 1);
+    return *reinterpret_cast<const float4 *>(P.conv + (size_t)t * kRowLen + off + d);
+}
+
+DIH_DEV void seq_load(SeqRegs &g, const DeltaParams &P, int t0, int head, int kh, int row0, int tid) {
+    const int last = P.tokens - 1;
+    g.k0 = seq_row4(P, t0, last, 0, tid, kK + kh * kDim);
+    g.k1 = seq_row4(P, t0, last, 1, tid, kK + kh * kDim);
+    g.k2 = seq_row4(P, t0, last, 2, tid, kK + kh * kDim);
+    g.k3 = seq_row4(P, t0, last, 3, tid, kK + kh * kDim);
+    g.q0 = seq_row4(P, t0, last, 0, tid, kQ + kh * kDim);
+    g.q1 = seq_row4(P, t0, last, 1, tid, kQ + kh * kDim);
+    g.q2 = seq_row4(P, t0, last, 2, tid, kQ + kh * kDim);
+    g.q3 = seq_row4(P, t0, last, 3, tid, kQ + kh * kDim);
+    const float *vrow = P.conv + kV + head * kDim + row0 + (tid & 15);
+    g.v0 = vrow[(size_t)min(t0 + (tid >> 4), last) * kRowLen];
+    g.v1 = vrow[(size_t)min(t0 + ((tid + 256) >> 4), last) * kRowLen];
+    const int t = min(t0 + (tid & 31), last);
+    g.ab = (tid < 32 ? P.decay : P.beta)[t * kVHeads + head];   // used by threads 0..63 only
+}
+
+DIH_DEV void seq_store(const SeqRegs &g, SeqStage &st, int tid) {
+    float4 *k = reinterpret_cast<float4 *>(st.k) + tid, *q = reinterpret_cast<float4 *>(st.q) + tid;
+    k[0] = g.k0; k[256] = g.k1; k[512] = g.k2; k[768] = g.k3;
+    q[0] = g.q0; q[256] = g.q1; q[512] = g.q2; q[768] = g.q3;
+    st.v[tid] = g.v0;
+    st.v[tid + 256] = g.v1;
+    if (tid < 32) st.a[tid] = g.ab;
+    else if (tid < 64) st.b[tid - 32] = g.ab;
+}
+
+struct TokenOps {
+    float4 k0, k1, q0, q1;
+    float a, b, v;
+};
+
+DIH_DEV void read_token(TokenOps &o, const SeqStage &st, int t, int sub, int rsub) {
+    const float4 *kp = reinterpret_cast<const float4 *>(&st.k[t * kDim + 8 * sub]);
+    const float4 *qp = reinterpret_cast<const float4 *>(&st.q[t * kDim + 8 * sub]);
+    o.k0 = kp[0]; o.k1 = kp[1];
+    o.q0 = qp[0]; o.q1 = qp[1];
+    o.a = st.a[t];
+    o.b = st.b[t];
+    o.v = st.v[t * 16 + rsub];
+}
+
+DIH_DEV float dot8(const float (&s)[8], float4 x0, float4 x1) {
+    return (s[0] * x0.x + s[1] * x0.y + s[2] * x0.z + s[3] * x0.w) +
+           (s[4] * x1.x + s[5] * x1.y + s[6] * x1.z + s[7] * x1.w);
+}
+
 __global__ __launch_bounds__(256) void delta_seq_kernel(DeltaParams P) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave, head = row >> 7, kh = head >> 1;
-    float *srow = P.state + (size_t)row * kDim;
-    float s0 = srow[lane], s1 = srow[lane + 64];
-    for (int t = 0; t < P.tokens; t++) {
-        const float *c = P.conv + (size_t)t * kRowLen;
-        const float a = P.decay[t * kVHeads + head], b = P.beta[t * kVHeads + head];
-        const float k0 = c[kK + kh * kDim + lane], k1 = c[kK + kh * kDim + lane + 64];
-        const float q0 = c[kQ + kh * kDim + lane], q1 = c[kQ + kh * kDim + lane + 64];
-        const float v = c[kV + row];
-        s0 *= a;
-        s1 *= a;
-        const float pred = wave_sum(s0 * k0 + s1 * k1);
-        const float corr = (v - pred) * b;
-        s0 += k0 * corr;
-        s1 += k1 * corr;
-        const float o = wave_sum(s0 * q0 + s1 * q1);
-        if (lane == 0) P.out[(size_t)t * (kVHeads * kDim) + row] = o;
+    __shared__ __align__(16) SeqStage stage[2];
+    const int tid = threadIdx.x, lane = tid & 63, sub = lane & 15, rsub = tid >> 4;
+    const int row0 = blockIdx.x * 16, row = row0 + rsub, head = row >> 7, kh = head >> 1;
+    const int hrow0 = row0 & (kDim - 1);
+    float4 *srow = reinterpret_cast<float4 *>(P.state + (size_t)row * kDim + 8 * sub);
+    float s[8];
+    {
+        const float4 a0 = srow[0], a1 = srow[1];
+        s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
     }
-    srow[lane] = s0;
-    srow[lane + 64] = s1;
-    if (blockIdx.x < kRowLen / 256) roll_history(P, blockIdx.x * 256 + threadIdx.x);
+    SeqRegs g;
+    seq_load(g, P, 0, head, kh, hrow0, tid);
+    seq_store(g, stage[0], tid);
+    __syncthreads();
+    for (int t0 = 0, buf = 0; t0 < P.tokens; t0 += kSeqChunk, buf ^= 1) {
+        const bool more = t0 + kSeqChunk < P.tokens;
+        if (more) seq_load(g, P, t0 + kSeqChunk, head, kh, hrow0, tid);
+        const SeqStage &st = stage[buf];
+        const int n = min(kSeqChunk, P.tokens - t0);
+        TokenOps cur, nxt;
+        read_token(cur, st, 0, sub, rsub);
+        for (int t = 0; t < n; t++) {
+            if (t + 1 < n) read_token(nxt, st, t + 1, sub, rsub);
+#pragma unroll
+            for (int i = 0; i < 8; i++) s[i] *= cur.a;
+            const float pred = group_sum(dot8(s, cur.k0, cur.k1), 16);
+            const float corr = (cur.v - pred) * cur.b;
+            const float kv[8] = {cur.k0.x, cur.k0.y, cur.k0.z, cur.k0.w, cur.k1.x, cur.k1.y, cur.k1.z, cur.k1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) s[i] += kv[i] * corr;
+            const float o = group_sum(dot8(s, cur.q0, cur.q1), 16);
+            if (sub == 0) P.out[(size_t)(t0 + t) * (kVHeads * kDim) + row] = o;
+            cur = nxt;
+        }
+        if (more) seq_store(g, stage[buf ^ 1], tid);   // the other buffer's readers finished a chunk ago
+        __syncthreads();
+    }
+    srow[0] = make_float4(s[0], s[1], s[2], s[3]);
+    srow[1] = make_float4(s[4], s[5], s[6], s[7]);
+    if (blockIdx.x < kRowLen / 256) roll_history(P, blockIdx.x * 256 + tid);
 }
 
 // ---- chunkwise prepare: one block per (head, 32-token block), 4 waves.
+constexpr int kPad4 = kDim + 4;   // f32 row stride of [32][128] tiles: 16-byte rows, conflict-free 128-bit reads
+constexpr int kSq4 = kBlk + 4;    // f32 row stride of [32][32] and [128][32] tiles, same property
+
+DIH_DEV void load_rows4(float *dst, const float *src_row0, int tid, int valid, int off) {
+    // [32][128] rows from the convolved rows (stride kRowLen) at column `off`; zero past `valid`
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i4 = tid + 256 * j, t = i4 >> 5, d = 4 * (i4 & 31);
+        // load the clamped row unconditionally and mask the value (a conditional load
+        // becomes a load through a selected pointer)
+        st4(dst + t * kPad4 + d, mask4(ld4(src_row0 + (size_t)min(t, valid - 1) * kRowLen + off + d), t < valid));
+    }
+}
+
 __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
-    __shared__ float ks[kBlk * kPad], qs[kBlk * kPad], vs[kBlk * kPad];
-    __shared__ float kk[kBlk * kSq], qk[kBlk * kSq], lt[kBlk * kSq], ti[kBlk * kSq];
-    __shared__ float a[kBlk], b[kBlk], g[kBlk];
+    __shared__ __align__(16) float ks[kBlk * kPad4], qs[kBlk * kPad4], vs[kBlk * kPad4];
+    __shared__ __align__(16) float kk[kBlk * kSq4], qk[kBlk * kSq4], lt[kBlk * kSq4], ti[kBlk * kSq4];
+    __shared__ __align__(16) float a[kBlk], b[kBlk], bg[kBlk];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, h = lane >> 5;
     const int head = blockIdx.x, blk = blockIdx.y, base = blk * kBlk, kh = head >> 1;
     const int valid = min(kBlk, P.tokens - base);
     const size_t tile = (size_t)blk * kVHeads + head;
+    const float *rows = P.conv + (size_t)base * kRowLen;
 
-    for (int i = tid; i < kBlk * kDim; i += 256) {
-        const int t = i >> 7, d = i & (kDim - 1);
-        const float *c = P.conv + (size_t)(base + t) * kRowLen;
-        const bool ok = t < valid;
-        ks[t * kPad + d] = ok ? c[kK + kh * kDim + d] : 0.f;
-        qs[t * kPad + d] = ok ? c[kQ + kh * kDim + d] : 0.f;
-        vs[t * kPad + d] = ok ? c[kV + head * kDim + d] : 0.f;
-    }
+    load_rows4(ks, rows, tid, valid, kK + kh * kDim);
+    load_rows4(qs, rows, tid, valid, kQ + kh * kDim);
+    load_rows4(vs, rows, tid, valid, kV + head * kDim);
     if (tid < kBlk) {
         a[tid] = tid < valid ? P.decay[(base + tid) * kVHeads + head] : 1.f;
         b[tid] = tid < valid ? P.beta[(base + tid) * kVHeads + head] : 0.f;
@@ -107,59 +215,76 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
         float p = 1.f, tail = 1.f;
         for (int j = 0; j <= tid; j++) p *= a[j];
         for (int j = tid + 1; j < valid; j++) tail *= a[j];
-        g[tid] = p;
+        bg[tid] = b[tid] * p;
         P.factors[(tile * kBlk + tid) * 2] = p;
         P.factors[(tile * kBlk + tid) * 2 + 1] = tid < valid ? tail : 0.f;
     }
-    // K K^T (wave 0) and Q K^T (wave 1): C[t][j] over 128 dims, 64 MFMAs each
+    // K K^T (wave 0) and Q K^T (wave 1) over 128 dims: MFMA s pairs dims (s, 64 + s), so a
+    // lane half reads 64 consecutive dims of its row, four per 128-bit read
     if (wave < 2) {
         const float *x = wave == 0 ? ks : qs;
-        dih_f32x16 acc;
+        dih_f32x16 acc0, acc1;
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[i] = 0.f;
-#pragma unroll 8
-        for (int s = 0; s < kDim / 2; s++)
-            acc = mfma_f32(x[r * kPad + 2 * s + h], ks[r * kPad + 2 * s + h], acc);
+        for (int i = 0; i < 16; i++) { acc0[i] = 0.f; acc1[i] = 0.f; }
+#pragma unroll 4
+        for (int m = 0; m < 16; m++) {
+            const f4 xa = ld4(x + r * kPad4 + 64 * h + 4 * m);
+            const f4 ka = ld4(ks + r * kPad4 + 64 * h + 4 * m);
+            acc0 = mfma_f32(xa[0], ka[0], acc0);
+            acc1 = mfma_f32(xa[1], ka[1], acc1);
+            acc0 = mfma_f32(xa[2], ka[2], acc0);
+            acc1 = mfma_f32(xa[3], ka[3], acc1);
+        }
         float *dst = wave == 0 ? kk : qk;
 #pragma unroll
-        for (int i = 0; i < 16; i++) dst[(8 * (i >> 2) + 4 * h + (i & 3)) * kSq + r] = acc[i];
+        for (int i = 0; i < 16; i++) dst[(8 * (i >> 2) + 4 * h + (i & 3)) * kSq4 + r] = acc0[i] + acc1[i];
     }
     __syncthreads();
-    // C (to global) and L (to LDS) with d(t,j) = a_{j+1}..a_t
-    for (int i = tid; i < kBlk * kBlk; i += 256) {
-        const int t = i >> 5, j = i & 31;
-        float d = 0.f;
-        if (t < valid && j <= t) {
-            d = 1.f;
-            for (int z = j + 1; z <= t; z++) d *= a[z];
+    // C (to global) and L (to LDS), lane j running d(t,j) = a_{j+1}..a_t down its column
+    if (tid < kBlk) {
+        const int j = tid;
+        float d = 1.f;
+#pragma unroll
+        for (int t = 0; t < kBlk; t++) {
+            if (t > j) d *= a[t];
+            const float dd = t < valid && j <= t ? d : 0.f;
+            P.causal[tile * (kBlk * kBlk) + t * kBlk + j] = qk[t * kSq4 + j] * dd;
+            lt[t * kSq4 + j] = t > j ? b[t] * dd * kk[t * kSq4 + j] : 0.f;
         }
-        P.causal[tile * (kBlk * kBlk) + i] = qk[t * kSq + j] * d;
-        lt[t * kSq + j] = t > j ? b[t] * d * kk[t * kSq + j] : 0.f;
     }
     __syncthreads();
-    // T = (I + L)^-1, lane c solving column c: T[t][c] = -(L[t][c] + sum_{c<j<t} L[t][j] T[j][c])
+    // T = (I + L)^-1, lane c solving column c in registers: x[t] = [t == c] for t <= c,
+    // x[t] = -sum_{j<t} L[t][j] x[j] after (x[j] = 0 for j < c, so the full sums are exact)
     if (tid < kBlk) {
         const int c = tid;
-        for (int t = 0; t < kBlk; t++) ti[t * kSq + c] = t == c ? 1.f : 0.f;
-        for (int t = c + 1; t < kBlk; t++) {
-            float sum = lt[t * kSq + c];
-            for (int j = c + 1; j < t; j++) sum += lt[t * kSq + j] * ti[j * kSq + c];
-            ti[t * kSq + c] = -sum;
+        float x[kBlk];
+#pragma unroll
+        for (int t = 0; t < kBlk; t++) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < t; j++) sum += lt[t * kSq4 + j] * x[j];
+            x[t] = t < c ? 0.f : t == c ? 1.f : -sum;
         }
+#pragma unroll
+        for (int t = 0; t < kBlk; t++) ti[t * kSq4 + c] = x[t];
     }
     __syncthreads();
-    // W = T diag(b g) K and U = T diag(b) V: wave w forms dims 32w..32w+31 of both
+    // W = T diag(b g) K and U = T diag(b) V: wave w forms dims 32w..32w+31 of both; MFMA s
+    // pairs tokens (s, 16 + s)
     {
         dih_f32x16 wa, ua;
 #pragma unroll
         for (int i = 0; i < 16; i++) { wa[i] = 0.f; ua[i] = 0.f; }
         const int dcol = 32 * wave + r;
-#pragma unroll 4
-        for (int s = 0; s < kBlk / 2; s++) {
-            const int j = 2 * s + h;
-            const float tj = ti[r * kSq + j];
-            wa = mfma_f32(tj, b[j] * g[j] * ks[j * kPad + dcol], wa);
-            ua = mfma_f32(tj, b[j] * vs[j * kPad + dcol], ua);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const f4 t4 = ld4(ti + r * kSq4 + 16 * h + 4 * m);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 16 * h + 4 * m + e;
+                wa = mfma_f32(t4[e], bg[j] * ks[j * kPad4 + dcol], wa);
+                ua = mfma_f32(t4[e], b[j] * vs[j * kPad4 + dcol], ua);
+            }
         }
         float *wt = P.w + tile * (kBlk * kDim), *ut = P.u + tile * (kBlk * kDim);
 #pragma unroll
@@ -175,10 +300,44 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
 // state's key dims 32w..32w+31 as S^T (C[m = dim][n = value row]), so every product
 // below takes the state, or the corrections D^T (same layout), as its B operand straight
 // from registers: the k-pair of each MFMA is (8j + c, 8j + 4 + c), which is register
-// 4j + c of both lane halves.
-__global__ __launch_bounds__(256) void delta_apply_kernel(DeltaParams P) {
-    __shared__ float ws[kBlk * kPad], gq[kBlk * kPad], tk[kBlk * kPad];
-    __shared__ float cs[kBlk * kSq];
+// 4j + c of both lane halves, and the matching A operands are four consecutive floats of
+// an LDS row (one 128-bit read per four MFMAs). The next block's operands are loaded into
+// registers while the current block computes.
+// (vector members, not arrays: a private array live across the loop is promoted to LDS,
+// which would store every prefetched value as soon as it arrives)
+struct BlockOps {
+    f4 w0, w1, w2, w3, q0, q1, q2, q3, k0, k1, k2, k3, c;
+    dih_f32x16 u;
+    float f;
+};
+
+DIH_DEV void load_block(BlockOps &o, const DeltaParams &P, int blk, int head, int kh, int row0, int tid, int r,
+                        int h) {
+    const int base = blk * kBlk, valid = min(kBlk, P.tokens - base);
+    const size_t tile = (size_t)blk * kVHeads + head;
+    const float *wt = P.w + tile * (kBlk * kDim);
+    auto rows = [&](int j, f4 &w, f4 &q, f4 &k) {
+        const int i4 = tid + 256 * j, t = i4 >> 5, d = 4 * (i4 & 31);
+        const float *c = P.conv + (size_t)(base + min(t, valid - 1)) * kRowLen;
+        w = ld4(wt + t * kDim + d);
+        q = mask4(ld4(c + kQ + kh * kDim + d), t < valid);
+        k = mask4(ld4(c + kK + kh * kDim + d), t < valid);
+    };
+    rows(0, o.w0, o.q0, o.k0);
+    rows(1, o.w1, o.q1, o.k1);
+    rows(2, o.w2, o.q2, o.k2);
+    rows(3, o.w3, o.q3, o.k3);
+    const float *cz = P.causal + tile * (kBlk * kBlk) + tid;
+    o.c = f4{cz[0], cz[256], cz[512], cz[768]};
+    o.f = P.factors[tile * kBlk * 2 + (tid & (2 * kBlk - 1))];   // used by threads 0..63
+    const float *ut = P.u + tile * (kBlk * kDim) + row0 + r;
+#pragma unroll
+    for (int i = 0; i < 16; i++) o.u[i] = ut[(8 * (i >> 2) + 4 * h + (i & 3)) * kDim];
+}
+
+__global__ __launch_bounds__(256, 1) void delta_apply_kernel(DeltaParams P) {
+    __shared__ __align__(16) float ws[kBlk * kPad4], qs[kBlk * kPad4], kt[kDim * kSq4];
+    __shared__ __align__(16) float cs[kBlk * kSq4], gf[kBlk], tl[kBlk];
     __shared__ __align__(16) float part[4][2][64 * 16];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, h = lane >> 5;
     const int head = blockIdx.x >> 2, row0 = (blockIdx.x & 3) * 32, kh = head >> 1;
@@ -189,61 +348,86 @@ __global__ __launch_bounds__(256) void delta_apply_kernel(DeltaParams P) {
 #pragma unroll
     for (int i = 0; i < 16; i++) st[i] = sbase[8 * (i >> 2) + 4 * h + (i & 3)];
 
+    BlockOps ops;
+    load_block(ops, P, 0, head, kh, row0, tid, r, h);
     for (int blk = 0; blk < P.nblocks; blk++) {
         const int base = blk * kBlk, valid = min(kBlk, P.tokens - base);
-        const size_t tile = (size_t)blk * kVHeads + head;
-        const float *fac = P.factors + tile * kBlk * 2;
         __syncthreads();   // the previous block's LDS reads are done
-        for (int i = tid; i < kBlk * kDim; i += 256) {
-            const int t = i >> 7, d = i & (kDim - 1);
-            const float *c = P.conv + (size_t)(base + t) * kRowLen;
-            const bool ok = t < valid;
-            ws[t * kPad + d] = P.w[tile * (kBlk * kDim) + i];
-            gq[t * kPad + d] = ok ? fac[2 * t] * c[kQ + kh * kDim + d] : 0.f;
-            tk[t * kPad + d] = ok ? fac[2 * t + 1] * c[kK + kh * kDim + d] : 0.f;
+        auto stage_rows = [&](int j, f4 w, f4 q, f4 k) {
+            const int i4 = tid + 256 * j, t = i4 >> 5, d = 4 * (i4 & 31);
+            st4(ws + t * kPad4 + d, w);
+            st4(qs + t * kPad4 + d, q);
+            kt[d * kSq4 + t] = k[0];          // keys transposed: [dim][token]
+            kt[(d + 1) * kSq4 + t] = k[1];
+            kt[(d + 2) * kSq4 + t] = k[2];
+            kt[(d + 3) * kSq4 + t] = k[3];
+        };
+        stage_rows(0, ops.w0, ops.q0, ops.k0);
+        stage_rows(1, ops.w1, ops.q1, ops.k1);
+        stage_rows(2, ops.w2, ops.q2, ops.k2);
+        stage_rows(3, ops.w3, ops.q3, ops.k3);
+        {
+            const int i = tid;
+            cs[(i >> 5) * kSq4 + (i & 31)] = ops.c[0];
+            cs[((i + 256) >> 5) * kSq4 + (i & 31)] = ops.c[1];
+            cs[((i + 512) >> 5) * kSq4 + (i & 31)] = ops.c[2];
+            cs[((i + 768) >> 5) * kSq4 + (i & 31)] = ops.c[3];
         }
-        for (int i = tid; i < kBlk * kBlk; i += 256) cs[(i >> 5) * kSq + (i & 31)] = P.causal[tile * (kBlk * kBlk) + i];
+        if (tid < 2 * kBlk) {
+            if (tid & 1) tl[tid >> 1] = ops.f;
+            else gf[tid >> 1] = ops.f;
+        }
+        const dih_f32x16 ucur = ops.u;
         __syncthreads();
+        if (blk + 1 < P.nblocks) load_block(ops, P, blk + 1, head, kh, row0, tid, r, h);
 
         // partial (over this wave's dims) W S^T and diag(g) Q S^T: C[m = token][n = row]
+        const float gr = gf[r];
         dih_f32x16 p1, p2;
 #pragma unroll
         for (int i = 0; i < 16; i++) { p1[i] = 0.f; p2[i] = 0.f; }
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int d = d0 + 8 * (i >> 2) + 4 * h + (i & 3);
-            p1 = mfma_f32(ws[r * kPad + d], st[i], p1);
-            p2 = mfma_f32(gq[r * kPad + d], st[i], p2);
+        for (int j = 0; j < 4; j++) {
+            const f4 wa = ld4(ws + r * kPad4 + d0 + 8 * j + 4 * h);
+            const f4 qa = ld4(qs + r * kPad4 + d0 + 8 * j + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                p1 = mfma_f32(wa[e], st[4 * j + e], p1);
+                p2 = mfma_f32(gr * qa[e], st[4 * j + e], p2);
+            }
         }
-        float4 *mine = reinterpret_cast<float4 *>(&part[wave][0][lane * 16]);
-        float4 *mine2 = reinterpret_cast<float4 *>(&part[wave][1][lane * 16]);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            mine[i] = make_float4(p1[4 * i], p1[4 * i + 1], p1[4 * i + 2], p1[4 * i + 3]);
-            mine2[i] = make_float4(p2[4 * i], p2[4 * i + 1], p2[4 * i + 2], p2[4 * i + 3]);
+            st4(&part[wave][0][lane * 16 + 4 * i], f4{p1[4 * i], p1[4 * i + 1], p1[4 * i + 2], p1[4 * i + 3]});
+            st4(&part[wave][1][lane * 16 + 4 * i], f4{p2[4 * i], p2[4 * i + 1], p2[4 * i + 2], p2[4 * i + 3]});
         }
-        __syncthreads();
-        // D^T = U^T - sum_waves(W S^T), the output's first term likewise
-        const float *ut = P.u + tile * (kBlk * kDim) + row0 + r;
+        // LDS writes visible, then a barrier without the memory fence: __syncthreads() would
+        // also wait for the next block's loads issued above
+        wait_lgkm0();
+        barrier_no_fence();
+        // D^T = U^T - sum_waves(W S^T); the output's first term likewise
         dih_f32x16 dd, o;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int t = 8 * (i >> 2) + 4 * h + (i & 3);
-            float s1 = 0.f, s2 = 0.f;
+        for (int i4 = 0; i4 < 4; i4++) {
+            f4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1;
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                s1 += part[w][0][lane * 16 + i];
-                s2 += part[w][1][lane * 16 + i];
+                s1 += ld4(&part[w][0][lane * 16 + 4 * i4]);
+                s2 += ld4(&part[w][1][lane * 16 + 4 * i4]);
             }
-            dd[i] = ut[t * kDim] - s1;
-            o[i] = s2;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                dd[4 * i4 + e] = ucur[4 * i4 + e] - s1[e];
+                o[4 * i4 + e] = s2[e];
+            }
         }
         // out = diag(g) Q S^T + C D, by one wave per block in turn
         if (wave == (blk & 3)) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int k = 8 * (i >> 2) + 4 * h + (i & 3);
-                o = mfma_f32(cs[r * kSq + k], dd[i], o);
+            for (int j = 0; j < 4; j++) {
+                const f4 ca = ld4(cs + r * kSq4 + 8 * j + 4 * h);
+#pragma unroll
+                for (int e = 0; e < 4; e++) o = mfma_f32(ca[e], dd[4 * j + e], o);
             }
             float *ob = P.out + (size_t)base * (kVHeads * kDim) + head * kDim + row0 + r;
 #pragma unroll
@@ -253,13 +437,15 @@ __global__ __launch_bounds__(256) void delta_apply_kernel(DeltaParams P) {
             }
         }
         // S^T <- g_last S^T + (tail o K)^T D^T
-        const float glast = fac[2 * (valid - 1)];
+        const float glast = gf[valid - 1];
 #pragma unroll
         for (int i = 0; i < 16; i++) st[i] *= glast;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int t = 8 * (i >> 2) + 4 * h + (i & 3);
-            st = mfma_f32(tk[t * kPad + d0 + r], dd[i], st);
+        for (int j = 0; j < 4; j++) {
+            const f4 ka = ld4(kt + (d0 + r) * kSq4 + 8 * j + 4 * h);
+            const f4 ta = ld4(tl + 8 * j + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; e++) st = mfma_f32(ta[e] * ka[e], dd[4 * j + e], st);
         }
     }
 #pragma unroll
@@ -277,7 +463,7 @@ bool launch_delta_rule(const DeltaArgs &a, hipStream_t s, char *error, int capac
     P.tokens = a.tokens;
     P.nblocks = (a.tokens + kBlk - 1) / kBlk;
     if (!a.chunked) {
-        DIH_LAUNCH(delta_seq_kernel, dim3(kVHeads * kDim / 4), dim3(256), 0, s, P);
+        DIH_LAUNCH(delta_seq_kernel, dim3(kVHeads * kDim / 16), dim3(256), 0, s, P);
         return hip_ok(hipGetLastError(), error, capacity, "delta launch");
     }
     if (!P.w || !P.u || !P.causal || !P.factors) {

@@ -49,19 +49,28 @@ struct Chunk {
     uint32_t w[BITS];  // 32 codes * BITS bits = BITS dwords
 };
 
-// Loads the 32-code chunk `chunk` (0-based, 32 columns each) of a row starting at `row`.
-template <int BITS>
+// Loads the 32-code chunk `chunk` (0-based, 32 columns each) of a row starting at `row`,
+// with the non-temporal hint (NT: the decode step's kernels, measured 0.5 % faster with
+// it) or plain loads (the long GEMV streams, measured 4-6 % faster without it).
+template <int BITS, bool NT = true>
 DIH_DEV void load_chunk(Chunk<BITS> &c, const uint32_t *row, int chunk) {
     const uint32_t *p = row + chunk * BITS;
     if constexpr (BITS == 8) {
         typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
         const u32x4 *q = reinterpret_cast<const u32x4 *>(p);
-        u32x4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+        u32x4 a, b;
+        if constexpr (NT) {
+            a = __builtin_nontemporal_load(q);
+            b = __builtin_nontemporal_load(q + 1);
+        } else {
+            a = q[0];
+            b = q[1];
+        }
         c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
         c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
     } else {
 #pragma unroll
-        for (int i = 0; i < BITS; i++) c.w[i] = __builtin_nontemporal_load(p + i);
+        for (int i = 0; i < BITS; i++) c.w[i] = NT ? __builtin_nontemporal_load(p + i) : p[i];
     }
 }
 

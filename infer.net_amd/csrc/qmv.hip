@@ -28,6 +28,7 @@ namespace dih {
 
 constexpr int kMaxSeg = 4;
 constexpr int kWavesTarget = 4096;   // 16 resident waves per CU on 256 CUs
+constexpr int kResidentWaves = 3072; // waves of the four-deep GEMV resident at once (3 per SIMD)
 
 struct QmvParams {
     QmvSeg seg[kMaxSeg];
@@ -139,7 +140,7 @@ DIH_DEV void xstage_store(const XStage<CPL> &X, const QmvSeg &S, uint32_t *lds) 
     }
 }
 
-template <int BITS, int CPL, bool GATED, int D, bool XH>
+template <int BITS, int CPL, bool GATED, int D, bool XH, bool PLAIN>
 DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_id, int wi, int W,
                       int K, bool active, const XStage<CPL> &X, uint32_t *lds) {
     const int lane = threadIdx.x & 63;
@@ -164,11 +165,11 @@ DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_i
         const uint32_t *wrow = S.p0 + rowi * wpr;
 #pragma unroll
         for (int c = 0; c < CPL; c++) {
-            load_chunk<BITS>(st.w[c], wrow, chc[c]);
+            load_chunk<BITS, !PLAIN>(st.w[c], wrow, chc[c]);
             st.s[c] = S.s0[rowi * gpr + (chc[c] >> 1)];
             st.b[c] = S.b0[rowi * gpr + (chc[c] >> 1)];
             if constexpr (GATED) {
-                load_chunk<BITS>(st.u[c], S.p1 + rowi * wpr, chc[c]);
+                load_chunk<BITS, !PLAIN>(st.u[c], S.p1 + rowi * wpr, chc[c]);
                 st.su[c] = S.s1[rowi * gpr + (chc[c] >> 1)];
                 st.bu[c] = S.b1[rowi * gpr + (chc[c] >> 1)];
             }
@@ -258,7 +259,8 @@ DIH_DEV void qmv_wave(const QmvSeg &S, int lpr, int slot, uint32_t e, bool bad_i
     }
 }
 
-template <int BITS, int CPL, int D>
+// PLAIN: plain weight loads for the long streams (the lm_head), non-temporal otherwise
+template <int BITS, int CPL, int D, bool PLAIN>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     extern __shared__ __align__(16) uint32_t qx[];   // the block's staged activations
     const int blk = blockIdx.x;
@@ -301,11 +303,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     if (bad_id) e = 0u;
     const bool xh = BITS == 8 && S.x_bf16;   // uniform over the block
     if (S.p1) {
-        if (xh) qmv_wave<BITS, CPL, true, D, BITS == 8>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
-        else qmv_wave<BITS, CPL, true, D, false>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+        if (xh) qmv_wave<BITS, CPL, true, D, BITS == 8, PLAIN>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+        else qmv_wave<BITS, CPL, true, D, false, PLAIN>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
     } else {
-        if (xh) qmv_wave<BITS, CPL, false, D, BITS == 8>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
-        else qmv_wave<BITS, CPL, false, D, false>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+        if (xh) qmv_wave<BITS, CPL, false, D, BITS == 8, PLAIN>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
+        else qmv_wave<BITS, CPL, false, D, false, PLAIN>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
     }
 }
 
@@ -341,8 +343,13 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
         total += groups[i] * segs[i].count;
     }
     // Row groups per wave: one while the launch has at most kWavesTarget row groups,
-    // else enough that the waves number about kWavesTarget.
-    const long per = std::max(1L, (total + kWavesTarget - 1) / kWavesTarget);
+    // else enough that the waves number about kWavesTarget. Long launches (the lm_head's
+    // 248,320 rows) size the wave count to what is resident at once instead, 3 waves per
+    // SIMD for the 160-VGPR four-deep ring (12 per CU on 256 CUs), so that no partial
+    // second round trails: measured 4 % faster there, slower for short launches.
+    const bool longrun = total > 4L * kWavesTarget;
+    const long target = longrun ? kResidentWaves : kWavesTarget;
+    const long per = std::max(1L, (total + target - 1) / target);
     int kmax = 1;
     int blocks = 0;
     for (int i = 0; i < nseg; i++) {
@@ -370,9 +377,17 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
     int maxc = 0;
     for (int i = 0; i < nseg; i++) maxc = std::max(maxc, segs[i].columns);
     const uint32_t lds = (uint32_t)maxc * 4 + (uint32_t)(maxc / 32) * 8;
+    // plain loads for long four-deep launches (measured 8 % faster on the lm_head, 5 %
+    // slower on a 4096-row GEMV, equal on the decode step)
+    const bool plain = longrun && depth == 4 && cpl == 1;
+    if (plain) {
+        if (bits == 8) DIH_LAUNCH((qmv_kernel<8, 1, 4, true>), grid, block, lds, s, P);
+        else DIH_LAUNCH((qmv_kernel<5, 1, 4, true>), grid, block, lds, s, P);
+        return hip_ok(hipGetLastError(), error, capacity, "qmv launch");
+    }
 #define DIH_QMV_CASE(B, C, D)                                                  \
     if (bits == B && cpl <= C && depth == D) {                                  \
-        DIH_LAUNCH((qmv_kernel<B, C, D>), grid, block, lds, s, P);             \
+        DIH_LAUNCH((qmv_kernel<B, C, D, false>), grid, block, lds, s, P);      \
         return hip_ok(hipGetLastError(), error, capacity, "qmv launch");       \
     }
     DIH_QMV_CASE(8, 1, 1) DIH_QMV_CASE(8, 1, 2) DIH_QMV_CASE(8, 1, 4)

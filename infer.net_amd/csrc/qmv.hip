@@ -28,7 +28,6 @@ namespace dih {
 
 constexpr int kMaxSeg = 4;
 constexpr int kWavesTarget = 4096;   // 16 resident waves per CU on 256 CUs
-constexpr int kResidentWaves = 3072; // waves of the four-deep GEMV resident at once (3 per SIMD)
 
 struct QmvParams {
     QmvSeg seg[kMaxSeg];
@@ -302,7 +301,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     const bool bad_id = e >= (uint32_t)S.experts;
     if (bad_id) e = 0u;
     const bool xh = BITS == 8 && S.x_bf16;   // uniform over the block
-    if (S.p1) {
+    if (!PLAIN && S.p1) {   // (long streams are single-matrix segments)
         if (xh) qmv_wave<BITS, CPL, true, D, BITS == 8, PLAIN>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
         else qmv_wave<BITS, CPL, true, D, false, PLAIN>(S, P.lpr[k], slot, e, bad_id, wi, W, P.iters[k], active, X, qx);
     } else {
@@ -344,12 +343,10 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
     }
     // Row groups per wave: one while the launch has at most kWavesTarget row groups,
     // else enough that the waves number about kWavesTarget. Long launches (the lm_head's
-    // 248,320 rows) size the wave count to what is resident at once instead, 3 waves per
-    // SIMD for the 160-VGPR four-deep ring (12 per CU on 256 CUs), so that no partial
-    // second round trails: measured 4 % faster there, slower for short launches.
+    // 248,320 rows) run the single-matrix kernel instance (102 VGPRs: four waves per SIMD,
+    // so all kWavesTarget waves are resident at once, no trailing partial round).
     const bool longrun = total > 4L * kWavesTarget;
-    const long target = longrun ? kResidentWaves : kWavesTarget;
-    const long per = std::max(1L, (total + target - 1) / target);
+    const long per = std::max(1L, (total + kWavesTarget - 1) / kWavesTarget);
     int kmax = 1;
     int blocks = 0;
     for (int i = 0; i < nseg; i++) {
@@ -377,9 +374,11 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
     int maxc = 0;
     for (int i = 0; i < nseg; i++) maxc = std::max(maxc, segs[i].columns);
     const uint32_t lds = (uint32_t)maxc * 4 + (uint32_t)(maxc / 32) * 8;
-    // plain loads for long four-deep launches (measured 8 % faster on the lm_head, 5 %
-    // slower on a 4096-row GEMV, equal on the decode step)
-    const bool plain = longrun && depth == 4 && cpl == 1;
+    // plain loads and the single-matrix instance for long four-deep launches (measured
+    // 107 -> 98 us on the lm_head; plain loads are 5 % slower on a 4096-row GEMV and equal
+    // on the decode step)
+    bool plain = longrun && depth == 4 && cpl == 1;
+    for (int i = 0; i < nseg; i++) plain = plain && !segs[i].p1;
     if (plain) {
         if (bits == 8) DIH_LAUNCH((qmv_kernel<8, 1, 4, true>), grid, block, lds, s, P);
         else DIH_LAUNCH((qmv_kernel<5, 1, 4, true>), grid, block, lds, s, P);

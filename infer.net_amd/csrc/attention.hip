@@ -6,8 +6,9 @@
 // head dim 256. Cache rows [position][kv head][256] bf16; queries [token][16][256] f32 or
 // bf16; gate source [token][16][512] (head h's gate at h*512+256); out [token][16][256].
 //
-// One block = 16 query tokens x the 8 heads of one KV head (128 rows) x one partition of
-// keys; each of its 4 waves owns 32 rows (4 tokens x 8 heads). Per 32-key tile:
+// One block = 16 query tokens (four waves, decode and short chunks) or 32 query tokens
+// (eight waves) x the 8 heads of one KV head x one partition of keys; each wave owns 32
+// rows (4 tokens x 8 heads). Per 32-key tile:
 //   S^T = K Q^T   16 v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = the wave's queries
 //                 held in registers as bf16); the accumulator layout gives every lane one
 //                 query row (lane & 31) and 16 of the tile's keys, so the row maximum and
@@ -77,28 +78,31 @@ DIH_DEV void store_out4(const AttnParams &P, int tok, int head, int d0, const fl
     }
 }
 
-// Keys reach LDS by direct global->LDS copies (no registers), double-buffered: key row kl
-// (512 B) holds its 16-byte piece c at slot c ^ (kl & 15), which makes the MFMA operand
-// reads (16 lanes = 16 keys, one piece each) conflict-free. Wave w copies rows 8w..8w+7, two
-// rows per instruction. Key indices past the partition end are clamped to its last key
-// (finite data; those keys are masked).
+// Keys reach LDS by direct global->LDS copies (no registers): key row kl (512 B) holds its
+// 16-byte piece c at slot c ^ (kl & 15), which makes the MFMA operand reads (16 lanes = 16
+// keys, one piece each) conflict-free. Of a block of NW waves, wave w copies rows
+// (32/NW)w .. (32/NW)(w+1)-1, two rows per instruction. Key indices past the partition end
+// are clamped to its last key (finite data; those keys are masked).
+template <int NW>
 DIH_DEV void issue_keys(const uint16_t *kbase, uint16_t *ksbuf, int kb, int kend, int wave, int lane) {
+    constexpr int RPW = kKeys / NW;   // rows per wave, two per copy instruction
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int kl = 8 * wave + 2 * i + (lane >> 5);
+    for (int i = 0; i < RPW / 2; i++) {
+        const int kl = RPW * wave + 2 * i + (lane >> 5);
         const int c = (lane & 31) ^ (kl & 15);
         const uint32_t key = (uint32_t)min(kb + kl, kend - 1);
         // 32-bit element offset from the wave-uniform base (the cache is below 2^31 elements)
         const uint32_t off = key * (uint32_t)(kKvHeads * kDim) + 8u * (uint32_t)c;
-        to_lds<16>(kbase + off, ksbuf + (8 * wave + 2 * i) * kDim);
+        to_lds<16>(kbase + off, ksbuf + (RPW * wave + 2 * i) * kDim);
     }
 }
 
 // Values reach LDS the same way, untransposed (raw rows of 512 B, piece c at slot
 // c ^ (kl & 15)), into one buffer that is consumed by the transpose below before the next
 // tile's copies are issued.
+template <int NW>
 DIH_DEV void issue_values(const uint16_t *vbase, uint16_t *vraw, int kb, int kend, int wave, int lane) {
-    issue_keys(vbase, vraw, kb, kend, wave, lane);
+    issue_keys<NW>(vbase, vraw, kb, kend, wave, lane);
 }
 
 DIH_DEV void store_vt_pair(uint16_t *vt, int d, int vq, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
@@ -128,6 +132,144 @@ DIH_DEV void transpose_values(const uint16_t *vraw, uint16_t *vt, int vq, int vc
     store_vt_pair(vt, d + 6, vq, v[0].w, v[1].w, v[2].w, v[3].w);
 }
 
+// The same for 512 threads: thread t reads 4 dims (4*(t/8)..+3) of keys 4*(t%8)..+3.
+DIH_DEV void transpose_values8(const uint16_t *vraw, uint16_t *vt, int t) {
+    const int vq = t & 7, vd = t >> 3;
+    uint2 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int kl = 4 * vq + i;
+        v[i] = *reinterpret_cast<const uint2 *>(vraw + kl * kDim + 8 * ((vd >> 1) ^ (kl & 15)) + 4 * (vd & 1));
+    }
+    // word x of each key holds dims 4vd (low half), 4vd+1; word y dims 4vd+2, 4vd+3
+    const uint32_t lo[4] = {v[0].x, v[1].x, v[2].x, v[3].x}, hi[4] = {v[0].y, v[1].y, v[2].y, v[3].y};
+    uint16_t *row = vt + 4 * vd * kVtStride + 4 * vq;
+    *reinterpret_cast<uint2 *>(row) = make_uint2(__builtin_amdgcn_perm(lo[1], lo[0], 0x05040100u),
+                                                 __builtin_amdgcn_perm(lo[3], lo[2], 0x05040100u));
+    *reinterpret_cast<uint2 *>(row + kVtStride) = make_uint2(__builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u),
+                                                             __builtin_amdgcn_perm(lo[3], lo[2], 0x07060302u));
+    *reinterpret_cast<uint2 *>(row + 2 * kVtStride) = make_uint2(__builtin_amdgcn_perm(hi[1], hi[0], 0x05040100u),
+                                                                 __builtin_amdgcn_perm(hi[3], hi[2], 0x05040100u));
+    *reinterpret_cast<uint2 *>(row + 3 * kVtStride) = make_uint2(__builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u),
+                                                                 __builtin_amdgcn_perm(hi[3], hi[2], 0x07060302u));
+}
+
+// ---- the parts of a wave's work shared by both block shapes. A wave owns 32 rows: 4
+// tokens x the 8 query heads of one KV head; lane (r, h) holds row r.
+
+// The wave's queries as MFMA B operands: qreg[s] = q[row][16s + 8h .. +8] in bf16.
+DIH_DEV void load_queries(dih_bf16x8 (&qreg)[16], const AttnParams &P, int my_tok, bool row_ok, int head, int h) {
+    const size_t qi = (size_t)(row_ok ? my_tok : 0) * (kHeads * kDim) + head * kDim + 8 * h;
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        uint4 u;
+        if (P.q_bf16) {
+            u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(P.q) + qi + 16 * s);
+        } else {
+            const float4 *f = reinterpret_cast<const float4 *>(static_cast<const float *>(P.q) + qi + 16 * s);
+            const float4 f0 = f[0], f1 = f[1];
+            u.x = pack_bf16x2(f0.x, f0.y); u.y = pack_bf16x2(f0.z, f0.w);
+            u.z = pack_bf16x2(f1.x, f1.y); u.w = pack_bf16x2(f1.z, f1.w);
+        }
+        if (!row_ok) u = make_uint4(0, 0, 0, 0);
+        qreg[s] = __builtin_bit_cast(dih_bf16x8, u);
+    }
+}
+
+// One 32-key tile (keys kb.., rows from ksb, values transposed in vtb) for the wave's rows.
+// `full`: every row of the wave sees the whole tile (no mask needed).
+DIH_DEV void attend_tile(const uint16_t *ksb, const uint16_t *vtb, const dih_bf16x8 (&qreg)[16],
+                         dih_f32x16 (&acc)[8], float &m_run, float &l_run, int kb, int kend, bool full,
+                         int my_last, int r, int h) {
+    // ---- S^T = K Q^T: s[k] is key kb + 8(k/4) + 4h + k%4 of row r
+    dih_f32x16 s;
+#pragma unroll
+    for (int k = 0; k < 16; k++) s[k] = 0.f;
+#pragma unroll
+    for (int st = 0; st < 16; st++) {
+        const dih_bf16x8 a = *reinterpret_cast<const dih_bf16x8 *>(ksb + r * kDim + 8 * ((2 * st + h) ^ (r & 15)));
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[st], s, 0, 0, 0);
+    }
+    // ---- online softmax for row r. Scores stay raw here; the log2 scale enters the
+    // exponent's FMA.
+    float mx = -INFINITY;
+    if (full) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) mx = fmaxf(mx, s[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int key = kb + 8 * (k >> 2) + 4 * h + (k & 3);
+            s[k] = key <= my_last && key < kend ? s[k] : -INFINITY;
+            mx = fmaxf(mx, s[k]);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx * kLog2eOver16);
+    const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;   // all keys masked so far: p = 0
+    float psum = 0.f;
+    uint32_t pw[8];
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k], kLog2eOver16, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[k + 1], kLog2eOver16, -m_use));
+        psum += p0 + p1;
+        pw[k >> 1] = pack_bf16x2(p0, p1);
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    // rescale only when some row's maximum moved (alpha == 1 exactly otherwise)
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc[dt][k] *= alpha;
+    }
+    const dih_bf16x8 pb0 = __builtin_bit_cast(dih_bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    const dih_bf16x8 pb1 = __builtin_bit_cast(dih_bf16x8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+    // ---- O^T = O^T * alpha + V^T P^T: acc[dt][k] is dim 32dt + 8(k/4) + 4h + k%4 of row r
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+        const uint16_t *vrow = vtb + (32 * dt + r) * kVtStride + 4 * h;
+        const uint2 a0 = *reinterpret_cast<const uint2 *>(vrow);
+        const uint2 a1 = *reinterpret_cast<const uint2 *>(vrow + 8);
+        const uint2 a2 = *reinterpret_cast<const uint2 *>(vrow + 16);
+        const uint2 a3 = *reinterpret_cast<const uint2 *>(vrow + 24);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(dih_bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y)), pb0, acc[dt], 0, 0, 0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(dih_bf16x8, make_uint4(a2.x, a2.y, a3.x, a3.y)), pb1, acc[dt], 0, 0, 0);
+    }
+}
+
+// The wave's rows after the partition: the output itself, or the partition's statistics
+// and unnormalized values for the combine.
+DIH_DEV void finish_rows(const AttnParams &P, const dih_f32x16 (&acc)[8], float m_run, float l_run, int my_tok,
+                         int head, int part, int h) {
+    if (P.nparts == 1) {
+        const float inv = 1.f / l_run;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float a4[4] = {acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]};
+                store_out4(P, my_tok, head, 32 * dt + 8 * i + 4 * h, a4, inv);
+            }
+    } else {
+        const size_t pi = ((size_t)my_tok * kHeads + head) * P.nparts + part;
+        if (h == 0) P.pstat[pi] = make_float2(m_run, l_run);
+        float *pa = P.pacc + pi * kDim;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                *reinterpret_cast<float4 *>(pa + 32 * dt + 8 * i + 4 * h) =
+                    make_float4(acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]);
+    }
+}
+
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
     __shared__ __align__(16) uint16_t ks[2][kKeys * kDim];
     __shared__ __align__(16) uint16_t vraw[kKeys * kDim];
@@ -154,25 +296,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
     const bool row_ok = my_tok < P.tokens;
     const int my_last = row_ok ? P.position + my_tok : -1;
 
-    // ---- the wave's queries as MFMA B operands: qreg[s] = q[row][16s + 8h .. +8] in bf16
     dih_bf16x8 qreg[16];
-    {
-        const size_t qi = (size_t)(row_ok ? my_tok : 0) * (kHeads * kDim) + head * kDim + 8 * h;
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-            uint4 u;
-            if (P.q_bf16) {
-                u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(P.q) + qi + 16 * s);
-            } else {
-                const float4 *f = reinterpret_cast<const float4 *>(static_cast<const float *>(P.q) + qi + 16 * s);
-                const float4 f0 = f[0], f1 = f[1];
-                u.x = pack_bf16x2(f0.x, f0.y); u.y = pack_bf16x2(f0.z, f0.w);
-                u.z = pack_bf16x2(f1.x, f1.y); u.w = pack_bf16x2(f1.z, f1.w);
-            }
-            if (!row_ok) u = make_uint4(0, 0, 0, 0);
-            qreg[s] = __builtin_bit_cast(dih_bf16x8, u);
-        }
-    }
+    load_queries(qreg, P, my_tok, row_ok, head, h);
 
     // ---- tiles are copied one compute phase ahead
     const uint16_t *kbase = P.keys + kh * kDim, *vbase = P.values + kh * kDim;
@@ -184,8 +309,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
 #pragma unroll
         for (int k = 0; k < 16; k++) acc[i][k] = 0.f;
 
-    issue_keys(kbase, ks[0], kstart, kend, wave, lane);
-    issue_values(vbase, vraw, kstart, kend, wave, lane);
+    issue_keys<4>(kbase, ks[0], kstart, kend, wave, lane);
+    issue_values<4>(vbase, vraw, kstart, kend, wave, lane);
     int buf = 0;
     for (int kb = kstart; kb < kend; kb += kKeys, buf ^= 1) {
         wait_vm<0>();             // this thread's copies have landed
@@ -193,98 +318,93 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
         transpose_values(vraw, vt, vq, vc);
         __syncthreads();          // vt complete, vraw consumed
         if (kb + kKeys < kend) {
-            issue_keys(kbase, ks[buf ^ 1], kb + kKeys, kend, wave, lane);
-            issue_values(vbase, vraw, kb + kKeys, kend, wave, lane);
+            issue_keys<4>(kbase, ks[buf ^ 1], kb + kKeys, kend, wave, lane);
+            issue_values<4>(vbase, vraw, kb + kKeys, kend, wave, lane);
         }
         if (!wave_ok || kb > wave_last) continue;
-
-        // ---- S^T = K Q^T: s[k] is key kb + 8(k/4) + 4h + k%4 of row r
-        dih_f32x16 s;
-#pragma unroll
-        for (int k = 0; k < 16; k++) s[k] = 0.f;
-#pragma unroll
-        for (int st = 0; st < 16; st++) {
-            const dih_bf16x8 a = *reinterpret_cast<const dih_bf16x8 *>(ks[buf] + r * kDim + 8 * ((2 * st + h) ^ (r & 15)));
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[st], s, 0, 0, 0);
-        }
-        // ---- online softmax for row r. Tiles every row of the wave sees whole (all but the
-        // diagonal and partition-end tiles) skip the mask. Scores stay raw here; the log2
-        // scale enters the exponent's FMA.
         const bool full = kb + kKeys - 1 <= P.position + wtok0 && kb + kKeys <= kend;
-        float mx = -INFINITY;
-        if (full) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) mx = fmaxf(mx, s[k]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const int key = kb + 8 * (k >> 2) + 4 * h + (k & 3);
-                s[k] = key <= my_last && key < kend ? s[k] : -INFINITY;
-                mx = fmaxf(mx, s[k]);
-            }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx * kLog2eOver16);
-        const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;   // all keys masked so far: p = 0
-        float psum = 0.f;
-        uint32_t pw[8];
-#pragma unroll
-        for (int k = 0; k < 16; k += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k], kLog2eOver16, -m_use));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[k + 1], kLog2eOver16, -m_use));
-            psum += p0 + p1;
-            pw[k >> 1] = pack_bf16x2(p0, p1);
-        }
-        psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        // rescale only when some row's maximum moved (alpha == 1 exactly otherwise)
-        if (__ballot(alpha != 1.f)) {
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-                for (int k = 0; k < 16; k++) acc[dt][k] *= alpha;
-        }
-        const dih_bf16x8 pb0 = __builtin_bit_cast(dih_bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        const dih_bf16x8 pb1 = __builtin_bit_cast(dih_bf16x8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
-        // ---- O^T = O^T * alpha + V^T P^T: acc[dt][k] is dim 32dt + 8(k/4) + 4h + k%4 of row r
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-            const uint16_t *vrow = vt + (32 * dt + r) * kVtStride + 4 * h;
-            const uint2 a0 = *reinterpret_cast<const uint2 *>(vrow);
-            const uint2 a1 = *reinterpret_cast<const uint2 *>(vrow + 8);
-            const uint2 a2 = *reinterpret_cast<const uint2 *>(vrow + 16);
-            const uint2 a3 = *reinterpret_cast<const uint2 *>(vrow + 24);
-            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(dih_bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y)), pb0, acc[dt], 0, 0, 0);
-            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(dih_bf16x8, make_uint4(a2.x, a2.y, a3.x, a3.y)), pb1, acc[dt], 0, 0, 0);
-        }
+        attend_tile(ks[buf], vt, qreg, acc, m_run, l_run, kb, kend, full, my_last, r, h);
     }
     if (!row_ok) return;
+    finish_rows(P, acc, m_run, l_run, my_tok, head, part, h);
+}
 
-    // ---- epilogue
-    if (P.nparts == 1) {
-        const float inv = 1.f / l_run;
+// ---- eight-wave form: 32 query tokens (256 rows) per block share each key/value tile.
+// Keys are triple-buffered and values double-buffered (raw copies and transposed), so one
+// barrier per tile suffices and every tile's copies are issued two tiles ahead:
+//   top of tile j: tile j's keys and transposed values are in LDS, tile j+1's copies landed
+//   issue tile j+2's copies (into the buffers tile j-1 used), compute tile j, transpose
+//   tile j+1's values, wait for this thread's copies, barrier.
+__global__ __launch_bounds__(512, 1) void attn8_kernel(AttnParams P) {
+    __shared__ __align__(16) uint16_t ks[3][kKeys * kDim];
+    __shared__ __align__(16) uint16_t vraw[2][kKeys * kDim];
+    __shared__ __align__(16) uint16_t vt[2][kDim * kVtStride];
+
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, r = lane & 31, h = lane >> 5;
+    // work item: as attn_kernel, with 32-token tiles
+    const int b = blockIdx.x, x = b & 7, kh = x >> 2;
+    const int idx = (x & 3) + 4 * (b >> 3);
+    if (idx >= P.ntiles * P.nparts) return;
+    const int tile = P.ntiles - 1 - idx / P.nparts, part = idx - (idx / P.nparts) * P.nparts;
+    const int tok0 = tile * (2 * kTok);
+    const int tok_hi = min(tok0 + 2 * kTok, P.tokens) - 1;
+    const int kstart = part * P.partition;
+    const int kend = min(kstart + P.partition, P.position + tok_hi + 1);
+    if (kstart >= kend) return;
+
+    const int wtok0 = tok0 + 4 * wave;
+    const bool wave_ok = wtok0 < P.tokens;
+    const int wave_last = P.position + min(wtok0 + 3, P.tokens - 1);
+    const int my_tok = wtok0 + (r >> 3), head = kh * kGroup + (r & 7);
+    const bool row_ok = my_tok < P.tokens;
+    const int my_last = row_ok ? P.position + my_tok : -1;
+
+    dih_bf16x8 qreg[16];
+    load_queries(qreg, P, my_tok, row_ok, head, h);
+    float m_run = -INFINITY, l_run = 0.f;
+    dih_f32x16 acc[8];
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++)
+    for (int i = 0; i < 8; i++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float a4[4] = {acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]};
-                store_out4(P, my_tok, head, 32 * dt + 8 * i + 4 * h, a4, inv);
-            }
+        for (int k = 0; k < 16; k++) acc[i][k] = 0.f;
+
+    const uint16_t *kbase = P.keys + kh * kDim, *vbase = P.values + kh * kDim;
+    const int ntile = (kend - kstart + kKeys - 1) / kKeys;
+    issue_keys<8>(kbase, ks[0], kstart, kend, wave, lane);
+    issue_values<8>(vbase, vraw[0], kstart, kend, wave, lane);
+    if (ntile > 1) {
+        issue_keys<8>(kbase, ks[1], kstart + kKeys, kend, wave, lane);
+        issue_values<8>(vbase, vraw[1], kstart + kKeys, kend, wave, lane);
+        wait_vm<4>();         // tile 0's four copies of this thread (tile 1's may stay in flight)
     } else {
-        const size_t pi = ((size_t)my_tok * kHeads + head) * P.nparts + part;
-        if (h == 0) P.pstat[pi] = make_float2(m_run, l_run);
-        float *pa = P.pacc + pi * kDim;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                *reinterpret_cast<float4 *>(pa + 32 * dt + 8 * i + 4 * h) =
-                    make_float4(acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]);
+        wait_vm<0>();
     }
+    barrier_no_fence();
+    transpose_values8(vraw[0], vt[0], t);
+    wait_vm<0>();
+    wait_lgkm0();
+    barrier_no_fence();
+
+    int k3 = 0;   // j % 3
+    for (int j = 0; j < ntile; j++) {
+        const int kb = kstart + j * kKeys;
+        if (j + 2 < ntile) {
+            const int k3n = k3 == 0 ? 2 : k3 - 1;   // (j + 2) % 3
+            issue_keys<8>(kbase, ks[k3n], kb + 2 * kKeys, kend, wave, lane);
+            issue_values<8>(vbase, vraw[j & 1], kb + 2 * kKeys, kend, wave, lane);
+        }
+        if (wave_ok && kb <= wave_last) {
+            const bool full = kb + kKeys - 1 <= P.position + wtok0 && kb + kKeys <= kend;
+            attend_tile(ks[k3], vt[j & 1], qreg, acc, m_run, l_run, kb, kend, full, my_last, r, h);
+        }
+        if (j + 1 < ntile) transpose_values8(vraw[(j + 1) & 1], vt[(j + 1) & 1], t);
+        wait_vm<0>();
+        wait_lgkm0();
+        barrier_no_fence();
+        k3 = k3 == 2 ? 0 : k3 + 1;
+    }
+    if (!row_ok) return;
+    finish_rows(P, acc, m_run, l_run, my_tok, head, part, h);
 }
 
 // One wave per (token, head), four dims per lane: merge the partitions that hold keys of
@@ -337,9 +457,15 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
 
 }  // namespace
 
+// Eight-wave blocks (32 tokens each) for chunks of more than one such tile; four-wave
+// blocks (16 tokens) for decode and short chunks, whose rows would mostly sit idle.
+static bool wide_blocks(int tokens) { return tokens > 2 * kTok; }
+
 int attention_partition(int position, int tokens, int requested) {
     if (requested > 0) return requested;
-    const int ntiles = (tokens + kTok - 1) / kTok;
+    const bool wide = wide_blocks(tokens);
+    const int tile_tokens = wide ? 2 * kTok : kTok;
+    const int ntiles = (tokens + tile_tokens - 1) / tile_tokens;
     const int keys = position + tokens;
     if (ntiles == 1) {
         // decode / short chunks: the key stream is latency-bound; about 128 partitions per
@@ -347,10 +473,11 @@ int attention_partition(int position, int tokens, int requested) {
         const int part = (((keys + 127) / 128) + 127) / 128 * 128;
         return part < 128 ? 128 : part;
     }
-    // (tile, KV head, partition) items: two blocks per CU of the 256-CU part, more when the
-    // keys are long (the partial results stay small against the key stream then)
+    // (tile, KV head, partition) items: two resident blocks per CU of the 256-CU part for
+    // four-wave blocks, one for eight-wave blocks; more when the keys are long (the
+    // partial results stay small against the key stream then)
     const int items = ntiles * kKvHeads;
-    const int target = 512 * std::min(4, std::max(1, keys / 8192));
+    const int target = (wide ? 256 : 512) * std::min(4, std::max(1, keys / 8192));
     if (items >= target) return ((keys + kKeys - 1) / kKeys) * kKeys;
     const int parts = (target + items - 1) / items;
     int part = (keys + parts - 1) / parts;
@@ -367,14 +494,18 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
     P.pacc = a.pacc; P.pstat = reinterpret_cast<float2 *>(a.pstat);
     P.position = a.position; P.tokens = a.tokens; P.partition = a.partition;
     P.nparts = (a.position + a.tokens + a.partition - 1) / a.partition;
-    P.ntiles = (a.tokens + kTok - 1) / kTok;
+    const bool wide = wide_blocks(a.tokens);
+    P.ntiles = (a.tokens + (wide ? 2 * kTok : kTok) - 1) / (wide ? 2 * kTok : kTok);
     if (P.nparts > 1 && (!P.pacc || !P.pstat)) {
         set_error(error, capacity, "Attention partitions need partial buffers");
         return false;
     }
     const int per = ((P.ntiles * P.nparts + 3) / 4) * 4;
     prof_stage("attention");
-    DIH_LAUNCH(attn_kernel, dim3(2 * per), dim3(256), 0, s, P);
+    if (wide)
+        DIH_LAUNCH(attn8_kernel, dim3(2 * per), dim3(512), 0, s, P);
+    else
+        DIH_LAUNCH(attn_kernel, dim3(2 * per), dim3(256), 0, s, P);
     if (!hip_ok(hipGetLastError(), error, capacity, "attention launch")) return false;
     if (P.nparts > 1) {
         prof_stage("attention_combine");

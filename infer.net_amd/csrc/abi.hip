@@ -983,17 +983,18 @@ __attribute__((visibility("default"))) int dih_delta_rule(void *ctx, float *stat
     a.conv = conv; a.decay = decay; a.beta = beta; a.raw = raw;
     a.state = state; a.history = history; a.out = out; a.tokens = tokens;
     // p_delta (gpu_prefill.mm:540-551) switches to the chunkwise form at 64 tokens; here the
-    // switch sits where the two measured equal on MI355X (sequential 55 us vs chunkwise 57 us
-    // at 192 tokens, 71 vs 68 us at 256)
-    constexpr int kChunkwiseFrom = 224;
+    // switch sits where the two measured equal on MI355X (sequential 26.7 us vs chunkwise
+    // 28.3 us at 80 tokens, 30.8 vs 28.5 us at 96)
+    constexpr int kChunkwiseFrom = 88;
     a.chunked = path == 0 ? tokens >= kChunkwiseFrom : path == 2;
     if (a.chunked) {
         const size_t blocks = ((size_t)tokens + 31) / 32, tiles = blocks * 32;
         a.w = static_cast<float *>(scratch(c, S_DW, tiles * 32 * 128 * 4, error, capacity));
         a.u = static_cast<float *>(scratch(c, S_DU, tiles * 32 * 128 * 4, error, capacity));
-        a.causal = static_cast<float *>(scratch(c, S_DC, tiles * 32 * 32 * 4, error, capacity));
+        a.qp = static_cast<float *>(scratch(c, S_DQ, tiles * 32 * 128 * 4, error, capacity));
+        a.cu = static_cast<float *>(scratch(c, S_DCU, tiles * 32 * 128 * 4, error, capacity));
         a.factors = static_cast<float *>(scratch(c, S_DF, tiles * 32 * 2 * 4, error, capacity));
-        if (!a.w || !a.u || !a.causal || !a.factors) return -1;
+        if (!a.w || !a.u || !a.qp || !a.cu || !a.factors) return -1;
     }
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);

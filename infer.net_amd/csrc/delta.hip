@@ -15,8 +15,12 @@
 //   W = T diag(b g) K,  U = T diag(b) V,  C = tril(d o Q K^T)
 //   D = U - W S^T                      (the block's corrections, one row per token)
 //   out = diag(g) Q S^T + C D,  S <- g_last S + D^T diag(g_last / g) K
-// prepare forms T, W, U, C per (head, block) in parallel; apply walks the blocks in order
-// with S resident in MFMA accumulators. All arithmetic is f32 (v_mfma_f32_32x32x2_f32).
+// prepare forms, per (head, block) in parallel, everything that does not involve S:
+//   W~ = diag(tail) W,  U~ = diag(tail) U   (tail = g_last / g, zero past the chunk)
+//   Q' = diag(g) Q - C W,  CU = C U
+// so that apply, walking the blocks in order with S resident in MFMA accumulators, only
+// forms D~ = U~ - W~ S^T = diag(tail) D,  out = Q' S^T + CU,  S <- g_last S + D~^T K.
+// All arithmetic is f32 (v_mfma_f32_32x32x2_f32 in prepare, 16x16x4 in apply).
 #include "dih_device.h"
 #include "dih_internal.h"
 
@@ -29,7 +33,7 @@ constexpr int kQ = 0, kK = 2048, kV = 4096;
 struct DeltaParams {
     const float *conv, *decay, *beta, *raw;
     float *state, *history, *out;
-    float *w, *u, *causal, *factors;   // chunkwise scratch, indexed by tile = block * 32 + head
+    float *w, *u, *qp, *cu, *factors;   // chunkwise scratch, indexed by tile = block * 32 + head
     int tokens, nblocks;
 };
 
@@ -178,6 +182,7 @@ __global__ __launch_bounds__(256) void delta_seq_kernel(DeltaParams P) {
 }
 
 // ---- chunkwise prepare: one block per (head, 32-token block), 4 waves.
+constexpr int kApplyRows = 16;   // value rows per apply block
 constexpr int kPad4 = kDim + 4;   // f32 row stride of [32][128] tiles: 16-byte rows, conflict-free 128-bit reads
 constexpr int kSq4 = kBlk + 4;    // f32 row stride of [32][32] and [128][32] tiles, same property
 
@@ -195,7 +200,7 @@ DIH_DEV void load_rows4(float *dst, const float *src_row0, int tid, int valid, i
 __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
     __shared__ __align__(16) float ks[kBlk * kPad4], qs[kBlk * kPad4], vs[kBlk * kPad4];
     __shared__ __align__(16) float kk[kBlk * kSq4], qk[kBlk * kSq4], lt[kBlk * kSq4], ti[kBlk * kSq4];
-    __shared__ __align__(16) float a[kBlk], b[kBlk], bg[kBlk];
+    __shared__ __align__(16) float a[kBlk], b[kBlk], bg[kBlk], gs[kBlk], tl[kBlk];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, h = lane >> 5;
     const int head = blockIdx.x, blk = blockIdx.y, base = blk * kBlk, kh = head >> 1;
     const int valid = min(kBlk, P.tokens - base);
@@ -216,6 +221,8 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
         for (int j = 0; j <= tid; j++) p *= a[j];
         for (int j = tid + 1; j < valid; j++) tail *= a[j];
         bg[tid] = b[tid] * p;
+        gs[tid] = p;
+        tl[tid] = tid < valid ? tail : 0.f;
         P.factors[(tile * kBlk + tid) * 2] = p;
         P.factors[(tile * kBlk + tid) * 2 + 1] = tid < valid ? tail : 0.f;
     }
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
         for (int i = 0; i < 16; i++) dst[(8 * (i >> 2) + 4 * h + (i & 3)) * kSq4 + r] = acc0[i] + acc1[i];
     }
     __syncthreads();
-    // C (to global) and L (to LDS), lane j running d(t,j) = a_{j+1}..a_t down its column
+    // C (over Q K^T in place) and L, lane j running d(t,j) = a_{j+1}..a_t down its column
     if (tid < kBlk) {
         const int j = tid;
         float d = 1.f;
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
         for (int t = 0; t < kBlk; t++) {
             if (t > j) d *= a[t];
             const float dd = t < valid && j <= t ? d : 0.f;
-            P.causal[tile * (kBlk * kBlk) + t * kBlk + j] = qk[t * kSq4 + j] * dd;
+            qk[t * kSq4 + j] *= dd;
             lt[t * kSq4 + j] = t > j ? b[t] * dd * kk[t * kSq4 + j] : 0.f;
         }
     }
@@ -286,171 +293,213 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
                 ua = mfma_f32(t4[e], b[j] * vs[j * kPad4 + dcol], ua);
             }
         }
-        float *wt = P.w + tile * (kBlk * kDim), *ut = P.u + tile * (kBlk * kDim);
+        // C W and C U: MFMA (j, e) pairs tokens (8j + e, 8j + 4 + e), which is register
+        // 4j + e of W and U in both lane halves
+        dih_f32x16 cw, cu;
+#pragma unroll
+        for (int i = 0; i < 16; i++) { cw[i] = 0.f; cu[i] = 0.f; }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f4 ca = ld4(qk + r * kSq4 + 8 * j + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                cw = mfma_f32(ca[e], wa[4 * j + e], cw);
+                cu = mfma_f32(ca[e], ua[4 * j + e], cu);
+            }
+        }
+        float *wt = P.w + tile * (kBlk * kDim), *qt = P.qp + tile * (kBlk * kDim);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int t = 8 * (i >> 2) + 4 * h + (i & 3);
-            wt[t * kDim + dcol] = wa[i];
-            ut[t * kDim + dcol] = ua[i];
+            wt[t * kDim + dcol] = tl[t] * wa[i];
+            qt[t * kDim + dcol] = gs[t] * qs[t * kPad4 + dcol] - cw[i];
+        }
+        // U~ and C U in the apply blocks' layout (value row c = 16 rg + n, token
+        // t = 16 tt + 4 g + i at [rg][tt][g][n][i]): registers 4q..4q+3 are four
+        // consecutive tokens of one column, one 16-byte store
+        const size_t cb = tile * (kBlk * kDim) + (dcol >> 4) * (kBlk * kApplyRows) + (dcol & 15) * 4;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int t0 = 8 * q + 4 * h, at = (t0 >> 4) * 256 + ((t0 >> 2) & 3) * 64;
+            st4(P.u + cb + at, f4{tl[t0] * ua[4 * q], tl[t0 + 1] * ua[4 * q + 1], tl[t0 + 2] * ua[4 * q + 2],
+                                  tl[t0 + 3] * ua[4 * q + 3]});
+            st4(P.cu + cb + at, f4{cu[4 * q], cu[4 * q + 1], cu[4 * q + 2], cu[4 * q + 3]});
         }
     }
 }
 
-// ---- chunkwise apply: one block per (head, 32 value rows), 4 waves; wave w holds the
-// state's key dims 32w..32w+31 as S^T (C[m = dim][n = value row]), so every product
-// below takes the state, or the corrections D^T (same layout), as its B operand straight
-// from registers: the k-pair of each MFMA is (8j + c, 8j + 4 + c), which is register
-// 4j + c of both lane halves, and the matching A operands are four consecutive floats of
-// an LDS row (one 128-bit read per four MFMAs). The next block's operands are loaded into
-// registers while the current block computes.
-// (vector members, not arrays: a private array live across the loop is promoted to LDS,
-// which would store every prefetched value as soon as it arrives)
-struct BlockOps {
-    f4 w0, w1, w2, w3, q0, q1, q2, q3, k0, k1, k2, k3, c;
-    dih_f32x16 u;
-    float f;
+// ---- chunkwise apply: one block per (head, 16 value rows), 256 blocks of 5 waves. Waves
+// 0..3 compute; wave w holds the state's key dims 32w..32w+31 as S^T in two 16x16 MFMA
+// accumulators (register i of lane l: dim 32w + 16mt + 4(l/16) + i, value row l%16). With
+// v_mfma_f32_16x16x4_f32 the k index of a product is the lane group l/16, so the k-steps
+// are chosen to take the state, or D~ (same layout), as the B operand straight from
+// registers: step (mt, i) covers dims 32w + 16mt + 4g + i (g = 0..3), and its A operands
+// are four consecutive floats of an LDS row (one 128-bit read per four MFMAs).
+//
+// Wave 4 only copies: a block's operands (W~, Q', K rows, the block's U~ and CU, the
+// factors: 53 KB) go global -> LDS directly (global_load_lds), double-buffered, the next
+// block's while the current one computes. The copies pass the CU's address unit at about
+// 64 bytes a clock, so a wave issuing them stalls for most of a block; a wave of their own
+// keeps those stalls off the MFMA waves. Rows of 128 floats are stored with 16-byte piece
+// p of row t at slot p ^ (t & 31), so both the 128-bit reads of a row segment and the
+// 32-bit reads of a key column are conflict-free. Rows past the chunk's end read the
+// chunk's last token: their W~, U~, Q' and CU rows are zero, so they add nothing to the
+// state or to the stored rows.
+struct ApplySet {
+    float w[kBlk * kDim], q[kBlk * kDim], k[kBlk * kDim];
+    float u[kBlk * kApplyRows], cu[kBlk * kApplyRows];   // [tt][g][n][i], as prepare writes them
+    float f[2 * kBlk];                                    // (g, tail) per token
 };
 
-DIH_DEV void load_block(BlockOps &o, const DeltaParams &P, int blk, int head, int kh, int row0, int tid, int r,
-                        int h) {
+DIH_DEV int slot128(int t, int p) { return 4 * (p ^ (t & 31)); }
+
+DIH_DEV f4 mfma16(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// A quarter of a block's copies, by copy wave c: row pairs 4c..4c+3 of W~, Q' and K, one
+// half of U~ (c = 0, 1) or CU (c = 2, 3); copy wave 0 also the 64 factors.
+DIH_DEV void copy_block(ApplySet &S, const DeltaParams &P, int blk, int head, int kh, int rg, int c, int lane) {
     const int base = blk * kBlk, valid = min(kBlk, P.tokens - base);
     const size_t tile = (size_t)blk * kVHeads + head;
-    const float *wt = P.w + tile * (kBlk * kDim);
-    auto rows = [&](int j, f4 &w, f4 &q, f4 &k) {
-        const int i4 = tid + 256 * j, t = i4 >> 5, d = 4 * (i4 & 31);
-        const float *c = P.conv + (size_t)(base + min(t, valid - 1)) * kRowLen;
-        w = ld4(wt + t * kDim + d);
-        q = mask4(ld4(c + kQ + kh * kDim + d), t < valid);
-        k = mask4(ld4(c + kK + kh * kDim + d), t < valid);
-    };
-    rows(0, o.w0, o.q0, o.k0);
-    rows(1, o.w1, o.q1, o.k1);
-    rows(2, o.w2, o.q2, o.k2);
-    rows(3, o.w3, o.q3, o.k3);
-    const float *cz = P.causal + tile * (kBlk * kBlk) + tid;
-    o.c = f4{cz[0], cz[256], cz[512], cz[768]};
-    o.f = P.factors[tile * kBlk * 2 + (tid & (2 * kBlk - 1))];   // used by threads 0..63
-    const float *ut = P.u + tile * (kBlk * kDim) + row0 + r;
+    const float *wt = P.w + tile * (kBlk * kDim), *qt = P.qp + tile * (kBlk * kDim);
 #pragma unroll
-    for (int i = 0; i < 16; i++) o.u[i] = ut[(8 * (i >> 2) + 4 * h + (i & 3)) * kDim];
+    for (int i = 0; i < 4; i++) {
+        const int pair = 4 * c + i, t = 2 * pair + (lane >> 5), p = (lane & 31) ^ (t & 31);
+        to_lds<16>(wt + t * kDim + 4 * p, S.w + 2 * pair * kDim);
+        to_lds<16>(qt + t * kDim + 4 * p, S.q + 2 * pair * kDim);
+        to_lds<16>(P.conv + (size_t)(base + min(t, valid - 1)) * kRowLen + kK + kh * kDim + 4 * p,
+                   S.k + 2 * pair * kDim);
+    }
+    const int half = c & 1;
+    const float *src = (c < 2 ? P.u : P.cu) + tile * (kBlk * kDim) + rg * (kBlk * kApplyRows) + 256 * half;
+    to_lds<16>(src + 4 * lane, (c < 2 ? S.u : S.cu) + 256 * half);
+    if (c == 0) to_lds<4>(P.factors + tile * (2 * kBlk) + lane, S.f);
 }
 
-__global__ __launch_bounds__(256, 1) void delta_apply_kernel(DeltaParams P) {
-    __shared__ __align__(16) float ws[kBlk * kPad4], qs[kBlk * kPad4], kt[kDim * kSq4];
-    __shared__ __align__(16) float cs[kBlk * kSq4], gf[kBlk], tl[kBlk];
-    __shared__ __align__(16) float part[4][2][64 * 16];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, h = lane >> 5;
-    const int head = blockIdx.x >> 2, row0 = (blockIdx.x & 3) * 32, kh = head >> 1;
-    const int d0 = 32 * wave;
+// The block's partial products of the four waves: D~ needs all of W~ S^T (eight 128-bit
+// reads: wave w2, token tile tt at byte offset 1024 (2 w2 + tt)), out one quarter of
+// Q' S^T (four 64-bit reads 2 KB apart).
+DIH_DEV void part_sums(const float *p1, const float *p2, f4 &d0, f4 &d1, dih_f32x2 &o) {
+    d0 = (ld4(p1) + ld4(p1 + 512)) + (ld4(p1 + 1024) + ld4(p1 + 1536));
+    d1 = (ld4(p1 + 256) + ld4(p1 + 768)) + (ld4(p1 + 1280) + ld4(p1 + 1792));
+    const dih_f32x2 *q = reinterpret_cast<const dih_f32x2 *>(p2);
+    o = (q[0] + q[256]) + (q[512] + q[768]);
+}
 
-    float *sbase = P.state + ((size_t)head * kDim + row0 + r) * kDim + d0;
-    dih_f32x16 st;
-#pragma unroll
-    for (int i = 0; i < 16; i++) st[i] = sbase[8 * (i >> 2) + 4 * h + (i & 3)];
+// One block on a compute wave, from the set `S` the copy wave filled.
+DIH_DEV void apply_block(const ApplySet &S, float (&part)[2][4][2][64 * 4], f4 (&st)[2], const DeltaParams &P,
+                         int blk, int head, int rg, int wave, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    const int base = blk * kBlk, valid = min(kBlk, P.tokens - base);
 
-    BlockOps ops;
-    load_block(ops, P, 0, head, kh, row0, tid, r, h);
-    for (int blk = 0; blk < P.nblocks; blk++) {
-        const int base = blk * kBlk, valid = min(kBlk, P.tokens - base);
-        __syncthreads();   // the previous block's LDS reads are done
-        auto stage_rows = [&](int j, f4 w, f4 q, f4 k) {
-            const int i4 = tid + 256 * j, t = i4 >> 5, d = 4 * (i4 & 31);
-            st4(ws + t * kPad4 + d, w);
-            st4(qs + t * kPad4 + d, q);
-            kt[d * kSq4 + t] = k[0];          // keys transposed: [dim][token]
-            kt[(d + 1) * kSq4 + t] = k[1];
-            kt[(d + 2) * kSq4 + t] = k[2];
-            kt[(d + 3) * kSq4 + t] = k[3];
-        };
-        stage_rows(0, ops.w0, ops.q0, ops.k0);
-        stage_rows(1, ops.w1, ops.q1, ops.k1);
-        stage_rows(2, ops.w2, ops.q2, ops.k2);
-        stage_rows(3, ops.w3, ops.q3, ops.k3);
-        {
-            const int i = tid;
-            cs[(i >> 5) * kSq4 + (i & 31)] = ops.c[0];
-            cs[((i + 256) >> 5) * kSq4 + (i & 31)] = ops.c[1];
-            cs[((i + 512) >> 5) * kSq4 + (i & 31)] = ops.c[2];
-            cs[((i + 768) >> 5) * kSq4 + (i & 31)] = ops.c[3];
+    // partial (over this wave's dims) W~ S^T and Q' S^T, token tiles tt: C[m = token][n = row];
+    // all eight operand reads first (the scheduler would otherwise wait on each pair just
+    // before its MFMAs)
+    f4 wa[2][2], qa[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const int t = 16 * tt + n, at = t * kDim + slot128(t, 8 * wave + 4 * mt + g);
+            wa[tt][mt] = ld4(S.w + at);
+            qa[tt][mt] = ld4(S.q + at);
         }
-        if (tid < 2 * kBlk) {
-            if (tid & 1) tl[tid >> 1] = ops.f;
-            else gf[tid >> 1] = ops.f;
-        }
-        const dih_f32x16 ucur = ops.u;
-        __syncthreads();
-        if (blk + 1 < P.nblocks) load_block(ops, P, blk + 1, head, kh, row0, tid, r, h);
-
-        // partial (over this wave's dims) W S^T and diag(g) Q S^T: C[m = token][n = row]
-        const float gr = gf[r];
-        dih_f32x16 p1, p2;
+    __builtin_amdgcn_sched_barrier(0);
+    f4 p1[2], p2[2];
 #pragma unroll
-        for (int i = 0; i < 16; i++) { p1[i] = 0.f; p2[i] = 0.f; }
+    for (int tt = 0; tt < 2; tt++) {
+        p1[tt] = f4{0.f, 0.f, 0.f, 0.f};
+        p2[tt] = p1[tt];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const f4 wa = ld4(ws + r * kPad4 + d0 + 8 * j + 4 * h);
-            const f4 qa = ld4(qs + r * kPad4 + d0 + 8 * j + 4 * h);
+        for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                p1 = mfma_f32(wa[e], st[4 * j + e], p1);
-                p2 = mfma_f32(gr * qa[e], st[4 * j + e], p2);
+            for (int i = 0; i < 4; i++) {
+                p1[tt] = mfma16(wa[tt][mt][i], st[mt][i], p1[tt]);
+                p2[tt] = mfma16(qa[tt][mt][i], st[mt][i], p2[tt]);
             }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            st4(&part[wave][0][lane * 16 + 4 * i], f4{p1[4 * i], p1[4 * i + 1], p1[4 * i + 2], p1[4 * i + 3]});
-            st4(&part[wave][1][lane * 16 + 4 * i], f4{p2[4 * i], p2[4 * i + 1], p2[4 * i + 2], p2[4 * i + 3]});
-        }
-        // LDS writes visible, then a barrier without the memory fence: __syncthreads() would
-        // also wait for the next block's loads issued above
-        wait_lgkm0();
-        barrier_no_fence();
-        // D^T = U^T - sum_waves(W S^T); the output's first term likewise
-        dih_f32x16 dd, o;
-#pragma unroll
-        for (int i4 = 0; i4 < 4; i4++) {
-            f4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                s1 += ld4(&part[w][0][lane * 16 + 4 * i4]);
-                s2 += ld4(&part[w][1][lane * 16 + 4 * i4]);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                dd[4 * i4 + e] = ucur[4 * i4 + e] - s1[e];
-                o[4 * i4 + e] = s2[e];
-            }
-        }
-        // out = diag(g) Q S^T + C D, by one wave per block in turn
-        if (wave == (blk & 3)) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const f4 ca = ld4(cs + r * kSq4 + 8 * j + 4 * h);
-#pragma unroll
-                for (int e = 0; e < 4; e++) o = mfma_f32(ca[e], dd[4 * j + e], o);
-            }
-            float *ob = P.out + (size_t)base * (kVHeads * kDim) + head * kDim + row0 + r;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int t = 8 * (i >> 2) + 4 * h + (i & 3);
-                if (t < valid) ob[(size_t)t * (kVHeads * kDim)] = o[i];
-            }
-        }
-        // S^T <- g_last S^T + (tail o K)^T D^T
-        const float glast = gf[valid - 1];
-#pragma unroll
-        for (int i = 0; i < 16; i++) st[i] *= glast;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const f4 ka = ld4(kt + (d0 + r) * kSq4 + 8 * j + 4 * h);
-            const f4 ta = ld4(tl + 8 * j + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; e++) st = mfma_f32(ta[e] * ka[e], dd[4 * j + e], st);
-        }
     }
+    // the state update's key operands, read ahead of the barrier: step (tt, i) covers tokens
+    // 16tt + 4g + i, tile mt dims 32w + 16mt + n
+    float ka[2][2][4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) sbase[8 * (i >> 2) + 4 * h + (i & 3)] = st[i];
-    if (blockIdx.x < kRowLen / 256) roll_history(P, blockIdx.x * 256 + tid);
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                const int t = 16 * tt + 4 * g + i, dim = 32 * wave + 16 * mt + n;
+                ka[tt][mt][i] = S.k[t * kDim + slot128(t, dim >> 2) + (dim & 3)];
+            }
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        st4(&part[0][wave][tt][lane * 4], p1[tt]);
+        st4(&part[1][wave][tt][lane * 4], p2[tt]);
+    }
+    wait_lgkm0();
+    barrier_no_fence();
+    // D~ = U~ - sum_waves(W~ S^T) in full; out = CU + sum_waves(Q' S^T) for this wave's
+    // quarter: token tile wave / 2, registers 2 (wave & 1) and 2 (wave & 1) + 1
+    const int ot = wave >> 1, oi = 2 * (wave & 1);
+    f4 s0, s1;
+    dih_f32x2 o;
+    part_sums(&part[0][0][0][lane * 4], &part[1][0][ot][lane * 4 + oi], s0, s1, o);
+    const f4 d0 = ld4(S.u + lane * 4) - s0, d1 = ld4(S.u + 256 + lane * 4) - s1;
+    o += *reinterpret_cast<const dih_f32x2 *>(S.cu + 256 * ot + lane * 4 + oi);
+    float *ob = P.out + (size_t)(base + 16 * ot + 4 * g + oi) * (kVHeads * kDim) + head * kDim + rg * kApplyRows + n;
+    if (16 * ot + 4 * g + oi < valid) ob[0] = o[0];
+    if (16 * ot + 4 * g + oi + 1 < valid) ob[kVHeads * kDim] = o[1];
+
+    // S^T <- g_last S^T + K^T D~: step (tt, i) covers tokens 16tt + 4g + i (the two state
+    // tiles' chains in turn: two chains keep the MFMA pipe full)
+    const float glast = S.f[2 * (valid - 1)];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) st[mt] *= glast;
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        const f4 d = tt ? d1 : d0;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) st[mt] = mfma16(ka[tt][mt][i], d[i], st[mt]);
+    }
+}
+
+// Blocks: XCD x (block b runs on XCD b % 8) takes value heads 2x, 2x + 1, 2x + 16, 2x + 17
+// (two key heads), eight row groups each, so the blocks sharing a head's W~, Q' and K
+// tiles share one L2. Two barriers a block: after the partial products (the sums need all
+// four), and at its end (the copy wave's copies of the next block have landed, and the
+// compute waves are done with this block's set and partial sums).
+__global__ __launch_bounds__(512, 1) void delta_apply_kernel(DeltaParams P) {
+    __shared__ __align__(16) ApplySet sets[2];
+    __shared__ __align__(16) float part[2][4][2][64 * 4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, hl = slot >> 3, rg = slot & 7;
+    const int head = 2 * xcd + (hl & 1) + 16 * (hl >> 1), kh = head >> 1;
+
+    // (barriers without the memory fence: __syncthreads() would make the copy wave wait for
+    // its copies at the mid-block barrier, and the compute waves for their row stores)
+    if (wave >= 4) {
+        copy_block(sets[0], P, 0, head, kh, rg, wave - 4, lane);
+        wait_vm<0>();
+        barrier_no_fence();
+        for (int blk = 0; blk < P.nblocks; blk++) {
+            if (blk + 1 < P.nblocks) copy_block(sets[(blk + 1) & 1], P, blk + 1, head, kh, rg, wave - 4, lane);
+            barrier_no_fence();
+            wait_vm<0>();
+            barrier_no_fence();
+        }
+    } else {
+        float *sbase =
+            P.state + ((size_t)head * kDim + rg * kApplyRows + (lane & 15)) * kDim + 32 * wave + 4 * (lane >> 4);
+        f4 st[2] = {ld4(sbase), ld4(sbase + 16)};
+        barrier_no_fence();
+        for (int blk = 0; blk < P.nblocks; blk++) {
+            apply_block(sets[blk & 1], part, st, P, blk, head, rg, wave, lane);
+            barrier_no_fence();
+        }
+        st4(sbase, st[0]);
+        st4(sbase + 16, st[1]);
+        if (blockIdx.x < kRowLen / 256) roll_history(P, blockIdx.x * 256 + tid);
+    }
 }
 
 }  // namespace
@@ -459,14 +508,14 @@ bool launch_delta_rule(const DeltaArgs &a, hipStream_t s, char *error, int capac
     DeltaParams P;
     P.conv = a.conv; P.decay = a.decay; P.beta = a.beta; P.raw = a.raw;
     P.state = a.state; P.history = a.history; P.out = a.out;
-    P.w = a.w; P.u = a.u; P.causal = a.causal; P.factors = a.factors;
+    P.w = a.w; P.u = a.u; P.qp = a.qp; P.cu = a.cu; P.factors = a.factors;
     P.tokens = a.tokens;
     P.nblocks = (a.tokens + kBlk - 1) / kBlk;
     if (!a.chunked) {
         DIH_LAUNCH(delta_seq_kernel, dim3(kVHeads * kDim / 16), dim3(256), 0, s, P);
         return hip_ok(hipGetLastError(), error, capacity, "delta launch");
     }
-    if (!P.w || !P.u || !P.causal || !P.factors) {
+    if (!P.w || !P.u || !P.qp || !P.cu || !P.factors) {
         set_error(error, capacity, "Chunkwise delta rule needs its scratch buffers");
         return false;
     }
@@ -474,7 +523,7 @@ bool launch_delta_rule(const DeltaArgs &a, hipStream_t s, char *error, int capac
     DIH_LAUNCH(delta_prepare_kernel, dim3(kVHeads, P.nblocks), dim3(256), 0, s, P);
     if (!hip_ok(hipGetLastError(), error, capacity, "delta prepare launch")) return false;
     prof_stage("delta_apply");
-    DIH_LAUNCH(delta_apply_kernel, dim3(kVHeads * 4), dim3(256), 0, s, P);
+    DIH_LAUNCH(delta_apply_kernel, dim3(kVHeads * (kDim / kApplyRows)), dim3(512), 0, s, P);
     return hip_ok(hipGetLastError(), error, capacity, "delta apply launch");
 }
 

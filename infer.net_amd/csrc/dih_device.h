@@ -17,6 +17,7 @@
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short dih_bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float dih_f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float dih_f32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float dih_f32x2;
 
 DIH_DEV float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 

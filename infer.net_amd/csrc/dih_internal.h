@@ -60,7 +60,7 @@ struct Context {
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_TICKETS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DC, S_DF, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_COUNT_
 };
 static_assert(S_COUNT_ <= (int)(sizeof(Context::ws) / sizeof(Scratch)), "scratch table too small");
 
@@ -219,12 +219,12 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
 
 // Gated delta rule over a chunk (delta.hip): state [32][128][128] f32 and history
 // [3][8192] f32 updated in place; conv/raw [tokens][8192], decay/beta [tokens][32], out
-// [tokens][4096], all f32. The chunkwise path needs w, u [ceil(tokens/32)*32*32*128],
-// causal [ceil(tokens/32)*32*32*32] and factors [ceil(tokens/32)*32*32*2] f32 scratch.
+// [tokens][4096], all f32. The chunkwise path needs w, u, qp, cu
+// [ceil(tokens/32)*32*32*128] and factors [ceil(tokens/32)*32*32*2] f32 scratch.
 struct DeltaArgs {
     const float *conv = nullptr, *decay = nullptr, *beta = nullptr, *raw = nullptr;
     float *state = nullptr, *history = nullptr, *out = nullptr;
-    float *w = nullptr, *u = nullptr, *causal = nullptr, *factors = nullptr;
+    float *w = nullptr, *u = nullptr, *qp = nullptr, *cu = nullptr, *factors = nullptr;
     int tokens = 0;
     int chunked = 0;
 };

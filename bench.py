@@ -363,7 +363,7 @@ class Bench:
         cases = [("chunk2048", 2048, 0), ("chunk2048_sequential", 2048, 1), ("chunk63", 63, 0),
                  ("chunk63_chunkwise", 63, 2), ("decode1", 1, 0)]
         if getattr(self.args, "delta_sweep", False):
-            cases += [(f"chunk{T}_{p}", T, i) for T in (64, 80, 96, 112, 128, 192, 256, 512, 1024)
+            cases += [(f"chunk{T}_{p}", T, i) for T in (32, 40, 48, 56, 64, 96, 128, 256, 512, 1024)
                       for i, p in ((1, "sequential"), (2, "chunkwise"))]
         for name, T, path in cases:
             g = torch.Generator(device="cuda").manual_seed(7)
@@ -509,7 +509,7 @@ def main():
     ap.add_argument("--workload", default="all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--delta-sweep", action="store_true", help="delta: both paths at 64..1024 tokens")
+    ap.add_argument("--delta-sweep", action="store_true", help="delta: both paths at 32..1024 tokens")
     ap.add_argument("--layers", type=int, default=24,
                     help="decode: rotating layer copies (24 x 855 MB keeps every step's weights out of the 256 MB MALL)")
     args = ap.parse_args()

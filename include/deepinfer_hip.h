@@ -269,8 +269,8 @@ int dih_attention_partition(int position, int tokens, int partition);
 /* Gated delta rule of a linear-attention (Gated DeltaNet) layer over a chunk of `tokens`
  * tokens: p_delta (gpu_prefill.mm:540-551), i.e. the sequential prefill_delta
  * (gpu_prefill.mm:177-191) or the chunkwise prefill_delta_prepare / prefill_delta_apply
- * (prefill_delta.mm:8-181); the library switches to the chunkwise form at 88 tokens (the
- * reference at 64), where the two cost the same on MI355X. For every token t, value
+ * (prefill_delta.mm:8-181); like the reference, the library switches to the chunkwise form
+ * at 64 tokens, which is also where the two cost the same on MI355X. For every token t, value
  * head h (32) and value row r (128), with key head h/2:
  *   S[h][r] *= decay[t][h];  c = (v - S[h][r].k) * beta[t][h];  S[h][r] += c k;
  *   out[t][h*128+r] = S[h][r].q

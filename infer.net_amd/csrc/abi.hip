@@ -982,10 +982,10 @@ __attribute__((visibility("default"))) int dih_delta_rule(void *ctx, float *stat
     DeltaArgs a;
     a.conv = conv; a.decay = decay; a.beta = beta; a.raw = raw;
     a.state = state; a.history = history; a.out = out; a.tokens = tokens;
-    // p_delta (gpu_prefill.mm:540-551) switches to the chunkwise form at 64 tokens; here the
-    // switch sits where the two measured equal on MI355X (sequential 26.7 us vs chunkwise
-    // 28.3 us at 80 tokens, 30.8 vs 28.5 us at 96)
-    constexpr int kChunkwiseFrom = 88;
+    // p_delta (gpu_prefill.mm:540-551) switches to the chunkwise form at 64 tokens, which is
+    // also where the two measured equal on MI355X (sequential 19.8 us vs chunkwise 20.1 us at
+    // 56 tokens, 22.1 vs 20.0 us at 64)
+    constexpr int kChunkwiseFrom = 64;
     a.chunked = path == 0 ? tokens >= kChunkwiseFrom : path == 2;
     if (a.chunked) {
         const size_t blocks = ((size_t)tokens + 31) / 32, tiles = blocks * 32;

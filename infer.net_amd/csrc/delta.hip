@@ -199,8 +199,11 @@ DIH_DEV void load_rows4(float *dst, const float *src_row0, int tid, int valid, i
 
 __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
     __shared__ __align__(16) float ks[kBlk * kPad4], qs[kBlk * kPad4], vs[kBlk * kPad4];
-    __shared__ __align__(16) float kk[kBlk * kSq4], qk[kBlk * kSq4], lt[kBlk * kSq4], ti[kBlk * kSq4];
+    // K K^T and Q K^T, each as two partial sums over the halves of the key dims; then C over
+    // the first Q K^T half, L over the first K K^T half, T over the second K K^T half
+    __shared__ __align__(16) float kkp[2][kBlk * kSq4], qkp[2][kBlk * kSq4];
     __shared__ __align__(16) float a[kBlk], b[kBlk], bg[kBlk], gs[kBlk], tl[kBlk];
+    float *const cs = qkp[0], *const lt = kkp[0], *const ti = kkp[1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, h = lane >> 5;
     const int head = blockIdx.x, blk = blockIdx.y, base = blk * kBlk, kh = head >> 1;
     const int valid = min(kBlk, P.tokens - base);
@@ -215,65 +218,109 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
         b[tid] = tid < valid ? P.beta[(base + tid) * kVHeads + head] : 0.f;
     }
     __syncthreads();
-    if (tid < kBlk) {
-        // g_t = a_0..a_t and the tail a_{t+1}..a_{valid-1}, both as direct products
-        float p = 1.f, tail = 1.f;
-        for (int j = 0; j <= tid; j++) p *= a[j];
-        for (int j = tid + 1; j < valid; j++) tail *= a[j];
-        bg[tid] = b[tid] * p;
-        gs[tid] = p;
-        tl[tid] = tid < valid ? tail : 0.f;
-        P.factors[(tile * kBlk + tid) * 2] = p;
-        P.factors[(tile * kBlk + tid) * 2 + 1] = tid < valid ? tail : 0.f;
-    }
-    // K K^T (wave 0) and Q K^T (wave 1) over 128 dims: MFMA s pairs dims (s, 64 + s), so a
-    // lane half reads 64 consecutive dims of its row, four per 128-bit read
-    if (wave < 2) {
-        const float *x = wave == 0 ? ks : qs;
+    // waves 0, 1: K K^T over dims [0, 64) and [64, 128); waves 2, 3: Q K^T likewise. MFMA
+    // (m, e) pairs dims (64hh + 4m + e, 64hh + 32 + 4m + e), lane half h taking the second,
+    // on two accumulator chains
+    {
+        const int hh = wave & 1;
+        const float *x = wave < 2 ? ks : qs;
         dih_f32x16 acc0, acc1;
 #pragma unroll
         for (int i = 0; i < 16; i++) { acc0[i] = 0.f; acc1[i] = 0.f; }
-#pragma unroll 4
-        for (int m = 0; m < 16; m++) {
-            const f4 xa = ld4(x + r * kPad4 + 64 * h + 4 * m);
-            const f4 ka = ld4(ks + r * kPad4 + 64 * h + 4 * m);
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int d = 64 * hh + 32 * h + 4 * m;
+            const f4 xa = ld4(x + r * kPad4 + d), ka = ld4(ks + r * kPad4 + d);
             acc0 = mfma_f32(xa[0], ka[0], acc0);
             acc1 = mfma_f32(xa[1], ka[1], acc1);
             acc0 = mfma_f32(xa[2], ka[2], acc0);
             acc1 = mfma_f32(xa[3], ka[3], acc1);
         }
-        float *dst = wave == 0 ? kk : qk;
+        float *dst = (wave < 2 ? kkp : qkp)[hh];
 #pragma unroll
         for (int i = 0; i < 16; i++) dst[(8 * (i >> 2) + 4 * h + (i & 3)) * kSq4 + r] = acc0[i] + acc1[i];
     }
     __syncthreads();
-    // C (over Q K^T in place) and L, lane j running d(t,j) = a_{j+1}..a_t down its column
-    if (tid < kBlk) {
-        const int j = tid;
+    // C and L, thread (j = column, rows 4q..4q+3); d(t,j) = a_{j+1}..a_t as a direct
+    // product, the decays held in registers
+    {
+        float ar[kBlk];
+#pragma unroll
+        for (int k4 = 0; k4 < kBlk / 4; k4++) {
+            const f4 v = ld4(a + 4 * k4);
+            ar[4 * k4] = v[0]; ar[4 * k4 + 1] = v[1]; ar[4 * k4 + 2] = v[2]; ar[4 * k4 + 3] = v[3];
+        }
+        const int j = tid & 31, t0 = 4 * (tid >> 5);
         float d = 1.f;
 #pragma unroll
-        for (int t = 0; t < kBlk; t++) {
-            if (t > j) d *= a[t];
+        for (int k = 1; k < kBlk; k++) d *= k > j && k <= t0 ? ar[k] : 1.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + i;
+            if (i > 0 && t > j) d *= a[t];
             const float dd = t < valid && j <= t ? d : 0.f;
-            qk[t * kSq4 + j] *= dd;
-            lt[t * kSq4 + j] = t > j ? b[t] * dd * kk[t * kSq4 + j] : 0.f;
+            const int at = t * kSq4 + j;
+            cs[at] = (qkp[0][at] + qkp[1][at]) * dd;
+            lt[at] = t > j ? b[t] * dd * (kkp[0][at] + kkp[1][at]) : 0.f;
+        }
+        // g_t = a_0..a_t and the tail a_{t+1}..a_{valid-1}, both as direct products
+        if (tid < kBlk) {
+            const int t = tid;
+            float p = 1.f, tail = 1.f;
+#pragma unroll
+            for (int k = 0; k < kBlk; k++) {
+                p *= k <= t ? ar[k] : 1.f;
+                tail *= k > t && k < valid ? ar[k] : 1.f;
+            }
+            bg[t] = b[t] * p;
+            gs[t] = p;
+            tl[t] = t < valid ? tail : 0.f;
+            P.factors[(tile * kBlk + t) * 2] = p;
+            P.factors[(tile * kBlk + t) * 2 + 1] = t < valid ? tail : 0.f;
         }
     }
     __syncthreads();
-    // T = (I + L)^-1, lane c solving column c in registers: x[t] = [t == c] for t <= c,
-    // x[t] = -sum_{j<t} L[t][j] x[j] after (x[j] = 0 for j < c, so the full sums are exact)
-    if (tid < kBlk) {
-        const int c = tid;
-        float x[kBlk];
+    // T = (I + L)^-1 by 16x16 blocks, on wave 0: lanes 0..15 and 16..31 invert the diagonal
+    // blocks column by column (x[t] = [t == c] for t <= c, x[t] = -sum_{j<t} L[t][j] x[j]
+    // after; x[j] = 0 for j < c, so the full sums are exact), then T21 = -T22 (L21 T11) on
+    // 16x16x4 MFMAs
+    if (wave == 0) {
+        if (lane < 32) {
+            const int o = 16 * (lane >> 4), c = lane & 15;
+            float x[16];
 #pragma unroll
-        for (int t = 0; t < kBlk; t++) {
-            float sum = 0.f;
+            for (int t = 0; t < 16; t++) {
+                float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-            for (int j = 0; j < t; j++) sum += lt[t * kSq4 + j] * x[j];
-            x[t] = t < c ? 0.f : t == c ? 1.f : -sum;
+                for (int j4 = 0; j4 < t; j4 += 4) {
+                    const f4 l4 = ld4(lt + (o + t) * kSq4 + o + j4);
+                    s0 += l4[0] * x[j4];
+                    if (j4 + 1 < t) s1 += l4[1] * x[j4 + 1];
+                    if (j4 + 2 < t) s0 += l4[2] * x[j4 + 2];
+                    if (j4 + 3 < t) s1 += l4[3] * x[j4 + 3];
+                }
+                x[t] = t < c ? 0.f : t == c ? 1.f : -(s0 + s1);
+            }
+#pragma unroll
+            for (int t = 0; t < 16; t++) {
+                ti[(o + t) * kSq4 + o + c] = x[t];
+                ti[(o == 0 ? t : t + 16) * kSq4 + (o == 0 ? 16 + c : c)] = 0.f;   // T12 = 0; T21 below
+            }
         }
+        wait_lgkm0();
+        // step s covers k = 4g + s (lane group g = lane / 16), so the product M = L21 T11 in
+        // its accumulator layout (register s: row 4g + s) is the B operand of the next
+        const int n = lane & 15, g = lane >> 4;
+        f4 m = {0.f, 0.f, 0.f, 0.f}, t21 = m;
 #pragma unroll
-        for (int t = 0; t < kBlk; t++) ti[t * kSq4 + c] = x[t];
+        for (int s = 0; s < 4; s++)
+            m = __builtin_amdgcn_mfma_f32_16x16x4f32(lt[(16 + n) * kSq4 + 4 * g + s], ti[(4 * g + s) * kSq4 + n], m,
+                                                     0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            t21 = __builtin_amdgcn_mfma_f32_16x16x4f32(ti[(16 + n) * kSq4 + 16 + 4 * g + s], m[s], t21, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) ti[(16 + 4 * g + i) * kSq4 + n] = -t21[i];
     }
     __syncthreads();
     // W = T diag(b g) K and U = T diag(b) V: wave w forms dims 32w..32w+31 of both; MFMA s
@@ -300,7 +347,7 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
         for (int i = 0; i < 16; i++) { cw[i] = 0.f; cu[i] = 0.f; }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const f4 ca = ld4(qk + r * kSq4 + 8 * j + 4 * h);
+            const f4 ca = ld4(cs + r * kSq4 + 8 * j + 4 * h);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 cw = mfma_f32(ca[e], wa[4 * j + e], cw);

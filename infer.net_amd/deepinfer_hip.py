@@ -564,7 +564,7 @@ def attention(dev, q, keys, values, gate, out, position, tokens, partition=0, q_
 
 def delta_rule(dev, state, history, conv, decay, beta, raw, out, tokens, path=0, stream=None) -> None:
     """Gated delta rule over a chunk (dih_delta_rule; p_delta, gpu_prefill.mm:540-551).
-    path 0: chunkwise from 88 tokens, sequential below (the library's choice); 1:
+    path 0: chunkwise from 64 tokens, sequential below (the library's choice); 1:
     sequential; 2: chunkwise."""
     err = _errbuf()
     _check(dev._lib.dih_delta_rule(_ctx(dev), _dp(state), _dp(history), _dp(conv), _dp(decay), _dp(beta),

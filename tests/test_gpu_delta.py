@@ -5,7 +5,7 @@ token-by-token recurrence oracle.delta_rule_f64, following prefill_delta_checks.
   .7*sin((t*11+h*17+d)*.013), state .01*sin(i*.003), history i*1e-4 (:10-15, :27-28);
 * four decay/beta modes: smooth, exact zeros and ones, 1e-15 decays, and .9999 with one
   key repeated over all tokens (:18-25);
-* token counts 1..2048 (:17), each on the library's path (sequential below 88 tokens,
+* token counts 1..2048 (:17), each on the library's path (sequential below 64 tokens,
   chunkwise from there) and the counts of the other path forced;
 * |out - oracle| <= 1e-5, relative L2 <= 3e-5, |state - oracle| <= 2e-5, history exact
   (:39-44).
@@ -97,15 +97,15 @@ def _check(got_out, got_state, want_out, want_state):
 @pytest.mark.parametrize("mode", [0, 1, 2, 3])
 @pytest.mark.parametrize("T", TOKENS)
 def test_delta_rule_against_recurrence(device, mode, T):
-    """The library's own path choice (sequential below 88 tokens, chunkwise from there)."""
+    """The library's own path choice (sequential below 64 tokens, chunkwise from there)."""
     _, _, _, _, outs, states = _oracle(mode)
     got_out, got_state, got_hist, hist, raw = _run(device, mode, T, 0)
     _check(got_out, got_state, outs[:T], states[T])
     assert np.array_equal(got_hist, orc.delta_history(hist, raw, T))
 
 
-@pytest.mark.parametrize("mode,T,path", [(0, 1, 2), (1, 3, 2), (2, 31, 2), (1, 32, 2), (3, 63, 2), (0, 64, 2),
-                                         (3, 65, 2), (2, 127, 1), (2, 128, 1), (3, 129, 1), (1, 256, 1),
+@pytest.mark.parametrize("mode,T,path", [(0, 1, 2), (1, 3, 2), (2, 31, 2), (1, 32, 2), (3, 63, 2), (0, 64, 1),
+                                         (3, 65, 1), (2, 127, 1), (2, 128, 1), (3, 129, 1), (1, 256, 1),
                                          (0, 513, 1)])
 def test_delta_rule_other_path(device, mode, T, path):
     """The path the library would not pick for this count: chunkwise for short chunks

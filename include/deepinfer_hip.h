@@ -250,9 +250,10 @@ int dih_dense(void *context, void *matrix, int tokens, const void *x, void *y, i
  *           sit at h*512+256 .. h*512+511
  *   out     [tokens][16][256] f32 or bf16:
  *           softmax(q.k/16 over keys 0..position+t) . v * sigmoid(gate)
- *   partition  keys per partition, a multiple of 32; 0 lets the library choose. Keys are
- *           scanned in 32-key blocks; probabilities are rounded to bf16 per block against
- *           the running maximum of their partition, as the reference rounds them.
+ *   partition  keys per partition, a multiple of 32; 0 lets the library choose (32 for one
+ *           token, which runs the decode kernel). Keys are scanned in 32-key blocks;
+ *           probabilities are rounded to bf16 per block against the running maximum of
+ *           their partition, as the reference rounds them.
  * Device pointers; runs on `stream` (NULL: the context's stream). Returns 0, or -1 with a
  * message when an argument is invalid (nothing is launched then). */
 int dih_attention(void *context, const void *q, int q_dtype, const uint16_t *keys,

@@ -455,6 +455,252 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
     store_out4(P, tok, head, 4 * lane, a4, 1.f / total);
 }
 
+// ---- decode (one query token): a block is four waves, each one 32-key tile of one KV
+// head (128 keys a block). Every tile is its own partition of 32 keys (the partition-32
+// rounding points: probabilities against the tile's maximum) and the block merges its four
+// as the combine does. A wave has no barrier before the merge: its keys (MFMA A operand),
+// values and queries are loaded straight into registers, 48 x 16 bytes a lane all in
+// flight at once, and only the values pass through LDS, to be transposed for O^T = V^T P^T.
+// Products are v_mfma_f32_16x16x32_bf16 (lane l: row l % 16, k = 8(l / 16)..+7; result
+// rows 4(l / 16) + i).
+constexpr int kDecKeys = 4 * kKeys;   // keys per decode block
+
+DIH_DEV dih_f32x4 mfma16_bf16(dih_bf16x8 a, dih_bf16x8 b, dih_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <bool QBF16>
+__global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
+    __shared__ __align__(16) uint16_t vt[4][kDim * kVtStride];   // per wave; its partial sums after
+    __shared__ __align__(16) uint16_t pb[4][16 * kKeys];         // per wave: bf16 probabilities [row][key]
+    __shared__ float2 stat[4][kGroup];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, n = lane & 15, g = lane >> 4;
+    // blocks dealt round-robin to the 8 XCDs: XCDs 0-3 take KV head 0, 4-7 KV head 1
+    const int b = blockIdx.x, x = b & 7, kh = x >> 2;
+    const int idx = (x & 3) + 4 * (b >> 3);
+    if (idx >= P.nparts) return;   // whole block
+    const int kend = P.position + 1;
+    const int kb = idx * kDecKeys + kKeys * wave;
+    const uint16_t *kbase = P.keys + kh * kDim, *vbase = P.values + kh * kDim;
+
+    // keys, the A operand: m-tile mt, k-step s: key kb + 16mt + n, dims 32s + 8g..+7
+    // (indices past the visible keys clamped to the last one; those scores are masked)
+    dih_bf16x8 ka[2][8];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        const uint32_t key = (uint32_t)min(kb + 16 * mt + n, kend - 1);
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            ka[mt][s] = *reinterpret_cast<const dih_bf16x8 *>(kbase + key * (uint32_t)(kKvHeads * kDim) + 32 * s + 8 * g);
+    }
+    // values for the transpose: keys kb + 4vq + i, dims 8vc..8vc+7, vc = lane / 8 + 8j
+    const int vq = lane & 7;
+    uint4 vv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t key = (uint32_t)min(kb + 4 * vq + i, kend - 1);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            vv[j][i] = *reinterpret_cast<const uint4 *>(vbase + key * (uint32_t)(kKvHeads * kDim) + 8 * ((lane >> 3) + 8 * j));
+    }
+    // queries, the B operand of S = K Q^T: lane (row n, g) holds dims 32s + 8g..+7 of head
+    // 8kh + n (rows 8..15 zero); loaded raw behind the keys and values, converted after, so
+    // that all of the wave's loads are in flight together
+    const int qhead = kh * kGroup + (n & 7);
+    // (rows 8..15 load nothing: a branch, so that their lanes are off for the loads)
+    float4 qf[8][2] = {};
+    uint4 qu[8] = {};
+    if (n < kGroup) {
+        if constexpr (QBF16) {
+            const uint16_t *qs = static_cast<const uint16_t *>(P.q) + (size_t)qhead * kDim + 8 * g;
+#pragma unroll
+            for (int s = 0; s < 8; s++) qu[s] = *reinterpret_cast<const uint4 *>(qs + 32 * s);
+        } else {
+            const float *qs = static_cast<const float *>(P.q) + (size_t)qhead * kDim + 8 * g;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                qf[s][0] = *reinterpret_cast<const float4 *>(qs + 32 * s);
+                qf[s][1] = *reinterpret_cast<const float4 *>(qs + 32 * s + 4);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dih_bf16x8 qb[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        uint4 u = qu[s];
+        if constexpr (!QBF16) {
+            u.x = pack_bf16x2(qf[s][0].x, qf[s][0].y); u.y = pack_bf16x2(qf[s][0].z, qf[s][0].w);
+            u.z = pack_bf16x2(qf[s][1].x, qf[s][1].y); u.w = pack_bf16x2(qf[s][1].z, qf[s][1].w);
+        }
+        if (n >= kGroup) u = make_uint4(0, 0, 0, 0);
+        qb[s] = __builtin_bit_cast(dih_bf16x8, u);
+    }
+
+    // ---- S = K Q^T: s[mt][i] is key kb + 16mt + 4g + i of row n
+    dih_f32x4 sc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        sc[mt] = dih_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; s++) sc[mt] = mfma16_bf16(ka[mt][s], qb[s], sc[mt]);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = kb + 16 * mt + 4 * g + i;
+            sc[mt][i] = key < kend ? sc[mt][i] : -INFINITY;
+            mx = fmaxf(mx, sc[mt][i]);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = mx * kLog2eOver16;
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a tile past the keys: p = 0
+    float psum = 0.f;
+    uint16_t *pbw = pb[wave];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p[i] = __builtin_amdgcn_exp2f(fmaf(sc[mt][i], kLog2eOver16, -m_use));
+            psum += p[i];
+        }
+        *reinterpret_cast<uint2 *>(pbw + n * kKeys + 16 * mt + 4 * g) =
+            make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
+    }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+
+    // ---- values transposed into the wave's LDS rows (dim d: its 32 keys, 72-byte rows)
+    uint16_t *vtw = vt[wave];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int d = 8 * ((lane >> 3) + 8 * j);
+        store_vt_pair(vtw, d, vq, vv[j][0].x, vv[j][1].x, vv[j][2].x, vv[j][3].x);
+        store_vt_pair(vtw, d + 2, vq, vv[j][0].y, vv[j][1].y, vv[j][2].y, vv[j][3].y);
+        store_vt_pair(vtw, d + 4, vq, vv[j][0].z, vv[j][1].z, vv[j][2].z, vv[j][3].z);
+        store_vt_pair(vtw, d + 6, vq, vv[j][0].w, vv[j][1].w, vv[j][2].w, vv[j][3].w);
+    }
+    // ---- O^T = V^T P^T: o[dt][i] is dim 16dt + 4g + i of row n
+    const dih_bf16x8 pk = *reinterpret_cast<const dih_bf16x8 *>(pbw + n * kKeys + 8 * g);
+    dih_f32x4 o[16];
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) {
+        const uint16_t *vrow = vtw + (16 * dt + n) * kVtStride + 8 * g;
+        const uint2 a0 = *reinterpret_cast<const uint2 *>(vrow), a1 = *reinterpret_cast<const uint2 *>(vrow + 4);
+        o[dt] = mfma16_bf16(__builtin_bit_cast(dih_bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y)), pk,
+                            dih_f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+    // ---- merge the four tiles: the partial sums of rows 0..7 go over the wave's own LDS
+    // rows (its reads of them are done: their values fed the MFMAs above)
+    float *accw = reinterpret_cast<float *>(vtw);   // [8 rows][256]
+    asm volatile("" ::: "memory");   // (the value rows above are read as uint16_t, written as float)
+    if (n < kGroup) {
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) *reinterpret_cast<dih_f32x4 *>(accw + n * kDim + 16 * dt + 4 * g) = o[dt];
+        if (g == 0) stat[wave][n] = make_float2(m_new, psum);
+    }
+    __syncthreads();
+    // thread: row t / 32, dims 8(t % 32)..+7
+    const int row = t >> 5, d0 = 8 * (t & 31);
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++) m = fmaxf(m, stat[w][row].x);
+    float total = 0.f, a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float2 st = stat[w][row];
+        const float wt = exp2f(st.x - m);   // 0 for a tile past the keys (max -inf)
+        total += wt * st.y;
+        const float *src = reinterpret_cast<const float *>(vt[w]) + row * kDim + d0;
+        const float4 u0 = *reinterpret_cast<const float4 *>(src), u1 = *reinterpret_cast<const float4 *>(src + 4);
+        a[0] += wt * u0.x; a[1] += wt * u0.y; a[2] += wt * u0.z; a[3] += wt * u0.w;
+        a[4] += wt * u1.x; a[5] += wt * u1.y; a[6] += wt * u1.z; a[7] += wt * u1.w;
+    }
+    const int head = kh * kGroup + row;
+    if (P.nparts == 1) {
+        const float a0[4] = {a[0], a[1], a[2], a[3]}, a1[4] = {a[4], a[5], a[6], a[7]};
+        store_out4(P, 0, head, d0, a0, 1.f / total);
+        store_out4(P, 0, head, d0 + 4, a1, 1.f / total);
+    } else {
+        const size_t pi = (size_t)head * P.nparts + idx;
+        if ((t & 31) == 0) P.pstat[pi] = make_float2(m, total);
+        float4 *pa = reinterpret_cast<float4 *>(P.pacc + pi * kDim + d0);
+        pa[0] = make_float4(a[0], a[1], a[2], a[3]);
+        pa[1] = make_float4(a[4], a[5], a[6], a[7]);
+    }
+}
+
+// Combine of many partitions (decode): block = (token, head, 32 dims); thread (partition
+// group pg = t / 8 of 32, dims 4(t % 8)..+3) sums every 32nd partition, then the groups
+// are summed through shuffles and LDS.
+__global__ __launch_bounds__(256) void attn_combine_wide_kernel(AttnParams P) {
+    __shared__ float red[4][8][5];
+    __shared__ float wmax[4];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int th = blockIdx.x >> 3, tok = th / kHeads, head = th - tok * kHeads;
+    const int d0 = 32 * (blockIdx.x & 7) + 4 * (t & 7), pg = t >> 3;
+    const int np = (P.position + tok) / P.partition + 1;
+    const size_t pi = (size_t)th * P.nparts;
+    const float2 *st = P.pstat + pi;
+    // eight of the group's partitions at a time, their loads issued together
+    constexpr int U = 8;
+    float m = -INFINITY;
+    float2 sv[U];
+    for (int p0 = pg; p0 < np; p0 += 32 * U) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int p = p0 + 32 * u;
+            sv[u] = st[min(p, np - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) m = fmaxf(m, sv[u].x);
+    }
+    m = wave_max(m);
+    if (lane == 0) wmax[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float total = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int p0 = pg; p0 < np; p0 += 32 * U) {
+        float4 av[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int p = min(p0 + 32 * u, np - 1);
+            sv[u] = st[p];
+            av[u] = *reinterpret_cast<const float4 *>(P.pacc + (pi + p) * kDim + d0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float w = p0 + 32 * u < np ? exp2f(sv[u].x - m) : 0.f;
+            total += w * sv[u].y;
+            acc.x += w * av[u].x; acc.y += w * av[u].y; acc.z += w * av[u].z; acc.w += w * av[u].w;
+        }
+    }
+    // the eight groups of a wave: lanes 8 apart
+#pragma unroll
+    for (int s = 8; s < 64; s <<= 1) {
+        total += __shfl_xor(total, s, 64);
+        acc.x += __shfl_xor(acc.x, s, 64); acc.y += __shfl_xor(acc.y, s, 64);
+        acc.z += __shfl_xor(acc.z, s, 64); acc.w += __shfl_xor(acc.w, s, 64);
+    }
+    if (lane < 8) {
+        red[wave][lane][0] = acc.x; red[wave][lane][1] = acc.y; red[wave][lane][2] = acc.z;
+        red[wave][lane][3] = acc.w; red[wave][lane][4] = total;
+    }
+    __syncthreads();
+    if (t < 8) {
+        float s5[5];
+#pragma unroll
+        for (int k = 0; k < 5; k++) s5[k] = red[0][t][k] + red[1][t][k] + red[2][t][k] + red[3][t][k];
+        const float a4[4] = {s5[0], s5[1], s5[2], s5[3]};
+        store_out4(P, tok, head, d0, a4, 1.f / s5[4]);
+    }
+}
+
 }  // namespace
 
 // Eight-wave blocks (32 tokens each) for chunks of more than one such tile; four-wave
@@ -463,6 +709,8 @@ static bool wide_blocks(int tokens) { return tokens > 2 * kTok; }
 
 int attention_partition(int position, int tokens, int requested) {
     if (requested > 0) return requested;
+    // one decode token: 32-key partitions (attn_decode_kernel)
+    if (tokens == 1) return kKeys;
     const bool wide = wide_blocks(tokens);
     const int tile_tokens = wide ? 2 * kTok : kTok;
     const int ntiles = (tokens + tile_tokens - 1) / tile_tokens;
@@ -499,6 +747,29 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
     if (P.nparts > 1 && (!P.pacc || !P.pstat)) {
         set_error(error, capacity, "Attention partitions need partial buffers");
         return false;
+    }
+    if (a.tokens == 1 && a.partition == kKeys) {
+        // decode: four 32-key partitions a block, merged there; the blocks' partial results
+        // are combined by (token, head, 32 dims)
+        P.partition = kDecKeys;
+        P.nparts = (a.position + 1 + kDecKeys - 1) / kDecKeys;
+        if (P.nparts > 1 && (!P.pacc || !P.pstat)) {
+            set_error(error, capacity, "Attention partitions need partial buffers");
+            return false;
+        }
+        prof_stage("attention");
+        const dim3 grid(2 * ((P.nparts + 3) / 4 * 4));
+        if (P.q_bf16)
+            DIH_LAUNCH(attn_decode_kernel<true>, grid, dim3(256), 0, s, P);
+        else
+            DIH_LAUNCH(attn_decode_kernel<false>, grid, dim3(256), 0, s, P);
+        if (!hip_ok(hipGetLastError(), error, capacity, "attention launch")) return false;
+        if (P.nparts > 1) {
+            prof_stage("attention_combine");
+            DIH_LAUNCH(attn_combine_wide_kernel, dim3(kHeads * 8), dim3(256), 0, s, P);
+            if (!hip_ok(hipGetLastError(), error, capacity, "attention combine launch")) return false;
+        }
+        return true;
     }
     const int per = ((P.ntiles * P.nparts + 3) / 4) * 4;
     prof_stage("attention");

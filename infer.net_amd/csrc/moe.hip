@@ -75,15 +75,18 @@ bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, u
 // ------------------------------------------------------------------------- grouping
 
 // Block e lists the routes r (= token*8 + slot) with ids[r] == e in ascending order
-// (prefill_build_groups prefill_moe.mm:8-17 uses a SIMD prefix sum per 32 routes; here a
-// 256-thread ballot/prefix pass per 256 routes). Block `experts` (when with_shared) lists
-// the shared expert's routes T*8 + t for every token. Blocks do not communicate: the GEMM
+// (prefill_build_groups prefill_moe.mm:8-17 uses a SIMD prefix sum per 32 routes). Here a
+// thread takes 64 consecutive routes a pass (16 K routes per pass of 256 threads, all its
+// loads issued together), counts its matches and places them after an add-scan of the
+// block's counts: one barrier per pass. Block `experts` (when with_shared) lists the
+// shared expert's routes T*8 + t for every token. Blocks do not communicate: the GEMM
 // derives its chunks from the counts (in expert order, so the order is deterministic where
 // the reference's atomic tile append, prefill_moe.mm:15, is not).
 __global__ __launch_bounds__(256) void group_kernel(const uint32_t *ids, int tokens, int experts,
                                                     int with_shared, uint32_t *counts,
                                                     uint32_t *routes) {
-    __shared__ uint32_t wave_tot[4];
+    constexpr int kPer = 64;   // routes per thread and pass
+    __shared__ uint32_t wave_tot[2][4];
     const int e = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T8 = tokens * 8;
@@ -94,20 +97,42 @@ __global__ __launch_bounds__(256) void group_kernel(const uint32_t *ids, int tok
         return;
     }
     uint32_t total = 0;
-    for (int base = 0; base < T8; base += 256) {
-        const int r = base + tid;
-        const bool sel = r < T8 && ids[r] == (uint32_t)e;
-        const unsigned long long mask = __ballot(sel);
-        const uint32_t below = (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_tot[wave] = (uint32_t)__popcll(mask);
+    int buf = 0;
+    for (int base = 0; base < T8; base += 256 * kPer, buf ^= 1) {
+        const int r0 = base + kPer * tid;
+        // 16-byte loads at clamped offsets (T8 is a multiple of 8), masked past the routes
+        uint4 v[kPer / 4];
+#pragma unroll
+        for (int k4 = 0; k4 < kPer / 4; k4++)
+            v[k4] = *reinterpret_cast<const uint4 *>(ids + min(r0 + 4 * k4, T8 - 4));
+        uint64_t hit = 0;
+#pragma unroll
+        for (int k4 = 0; k4 < kPer / 4; k4++) {
+            if (r0 + 4 * k4 >= T8) continue;
+            const uint64_t h = (uint64_t)(v[k4].x == (uint32_t)e) | (uint64_t)(v[k4].y == (uint32_t)e) << 1 |
+                               (uint64_t)(v[k4].z == (uint32_t)e) << 2 | (uint64_t)(v[k4].w == (uint32_t)e) << 3;
+            hit |= h << (4 * k4);
+        }
+        const uint32_t cnt = (uint32_t)__popcll(hit);
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        if (lane == 63) wave_tot[buf][wave] = incl;
         __syncthreads();
-        uint32_t off = total;
-        for (int w = 0; w < wave; w++) off += wave_tot[w];
+        uint32_t off = total + incl - cnt;
+        for (int w = 0; w < wave; w++) off += wave_tot[buf][w];
         // A token lists an expert at most once, so count <= tokens; ids that repeat an
         // expert within a token are truncated here instead of overrunning the list.
-        if (sel && off + below < (uint32_t)tokens) out[off + below] = (uint32_t)r;
-        total += wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
-        __syncthreads();
+        while (hit) {
+            const int k = __builtin_ctzll(hit);
+            hit &= hit - 1;
+            if (off < (uint32_t)tokens) out[off] = (uint32_t)(r0 + k);
+            off++;
+        }
+        total += wave_tot[buf][0] + wave_tot[buf][1] + wave_tot[buf][2] + wave_tot[buf][3];
     }
     if (tid == 0) counts[e] = min(total, (uint32_t)tokens);
 }

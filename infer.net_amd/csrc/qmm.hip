@@ -355,18 +355,23 @@ constexpr int qmm_lds_occupancy() {
 // SPLIT (gated only): eight waves, waves 0-3 the gate matrix and 4-7 the up matrix of the
 // same four 32-row slabs, so that two waves share each SIMD and one's dequant overlaps the
 // other's MFMAs and waits; the SwiGLU epilogue meets the two halves in LDS.
-template <int BITS, bool GATED, int NT, int S, bool SPLIT>
-__global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
+// RS (dense only): 32-row slabs per wave, so a block's row tile is 128*RS rows. Two slabs
+// double the MFMA work per activation tile read from LDS (each wave reads the whole tile
+// every step), which otherwise costs as much LDS bandwidth as the MFMAs take time.
+template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1>
+__global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
     static_assert(!SPLIT || GATED, "only the gated kernel splits its matrices over waves");
+    static_assert(RS == 1 || (!GATED && !SPLIT), "two slabs a wave: non-gated only");
+    constexpr int TR = 128 * RS;             // rows per row tile
     constexpr int NW = SPLIT ? 8 : 4;        // waves per block
     constexpr int BN = 32 * NT;
     constexpr int AB = 64 * BITS / 8;        // bytes of one row's codes per K step
-    constexpr int A_ST = 128 * AB;           // one matrix, one stage
+    constexpr int A_ST = TR * AB;            // one matrix, one stage
     constexpr int NMAT = GATED ? 2 : 1;
     constexpr int WMAT = SPLIT ? 1 : NMAT;   // matrices one wave dequantizes
     constexpr int B_ST = BN * 128;
     constexpr int ST = NMAT * A_ST + B_ST;   // bytes per stage
-    constexpr int AQ = BITS == 8 ? 2 : 5;    // direct copies per wave per matrix per step
+    constexpr int AQ = (BITS == 8 ? 2 : 5) * RS;   // direct copies per wave per matrix per step
     constexpr int NBW = 4 * NT / NW;         // activation copies (8 routes each) per wave
     static_assert(NBW >= 1 && NBW * NW == 4 * NT, "activation pieces split evenly over the waves");
     constexpr int LPS = WMAT * AQ + NBW;     // copies per thread per step
@@ -425,7 +430,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
     const size_t ebase = (size_t)(shared ? 0 : e) * R;
     const size_t row_bytes = (size_t)C * BITS / 8;
     auto row_index = [&](int rt, int rb) {  // (row tile, row in tile) -> matrix row (clamped)
-        const int row = rt * 128 + rb;
+        const int row = rt * TR + rb;
         return ebase + (row < R ? row : R - 1);
     };
     // this lane's copy rows within a tile and byte offsets within a row's K-step segment
@@ -434,23 +439,26 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
     for (int q = 0; q < AQ; q++) {
         if constexpr (BITS == 8) {
             const int rl = 16 * q + (lane >> 2), sl = lane & 3;
-            crow[q] = slab * 32 + rl;
+            crow[q] = slab * 32 * RS + rl;
             coff[q] = 16 * (sl ^ ((rl >> 2) & 3));
         } else {
             const int i = 64 * q + lane, rl = i / 10;
-            crow[q] = slab * 32 + rl;
+            crow[q] = slab * 32 * RS + rl;
             coff[q] = 4 * (i - rl * 10);
         }
     }
     // this lane's MFMA row; its scale/bias bf16 bits come eight groups per 16-byte load
     const int r = lane & 31, h = lane >> 5;
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-    auto win_load = [&](u32x4 (&sw)[2][2], int ti, int w) {
-        const size_t mrow = row_index(rt0 + ti, slab * 32 + r);
+    auto win_load = [&](u32x4 (&sw)[RS][2][2], int ti, int w) {
 #pragma unroll
-        for (int m = 0; m < WMAT; m++) {
-            sw[m][0] = *reinterpret_cast<const u32x4 *>(psc[m + mw] + mrow * G + 8 * w);
-            sw[m][1] = *reinterpret_cast<const u32x4 *>(pbi[m + mw] + mrow * G + 8 * w);
+        for (int rs = 0; rs < RS; rs++) {
+            const size_t mrow = row_index(rt0 + ti, slab * 32 * RS + 32 * rs + r);
+#pragma unroll
+            for (int m = 0; m < WMAT; m++) {
+                sw[rs][m][0] = *reinterpret_cast<const u32x4 *>(psc[m + mw] + mrow * G + 8 * w);
+                sw[rs][m][1] = *reinterpret_cast<const u32x4 *>(pbi[m + mw] + mrow * G + 8 * w);
+            }
         }
     };
 
@@ -481,9 +489,9 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
             for (int q = 0; q < AQ; q++) {
                 const char *src = pw[m] + row_index(rt0 + ti, crow[q]) * row_bytes + (size_t)kg * AB + coff[q];
                 if constexpr (BITS == 8)
-                    to_lds<16>(src, base + m * A_ST + (slab * 32 + 16 * q) * 64);
+                    to_lds<16>(src, base + m * A_ST + (slab * 32 * RS + 16 * q) * 64);
                 else
-                    to_lds<4>(src, base + m * A_ST + slab * 32 * 40 + q * 256);
+                    to_lds<4>(src, base + m * A_ST + slab * 32 * RS * 40 + q * 256);
             }
         }
 #pragma unroll
@@ -492,16 +500,18 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
 
 #pragma unroll
     for (int st = 0; st < S - 1; st++) issue(st, st);
-    u32x4 win[2][2], win_next[2][2];
+    u32x4 win[RS][2][2], win_next[RS][2][2];
     win_load(win, 0, 0);
 
-    dih_f32x16 acc0[NT], acc1[GATED && !SPLIT ? NT : 1];
+    dih_f32x16 acc0[RS][NT], acc1[GATED && !SPLIT ? NT : 1];
     auto zero_acc = [&]() {
 #pragma unroll
-        for (int i = 0; i < NT; i++) {
+        for (int rs = 0; rs < RS; rs++)
 #pragma unroll
-            for (int k = 0; k < 16; k++) acc0[i][k] = 0.f;
-        }
+            for (int i = 0; i < NT; i++) {
+#pragma unroll
+                for (int k = 0; k < 16; k++) acc0[rs][i][k] = 0.f;
+            }
         if constexpr (GATED && !SPLIT) {
 #pragma unroll
             for (int i = 0; i < NT; i++) {
@@ -524,26 +534,29 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
                 barrier_no_fence();
                 issue(step + S - 1, (u + S - 1) % S);
                 const unsigned char *base = stage_base(u % S);
-                // this step's weights -> bf16 A operands
-                dih_bf16x8 a[2][4];
+                // this step's weights -> bf16 A operands (a[rs * WMAT + m]: slab rs, matrix m)
+                dih_bf16x8 a[RS * 2][4];
+#pragma unroll
+                for (int rs = 0; rs < RS; rs++)
 #pragma unroll
                 for (int m = 0; m < WMAT; m++) {
                     Chunk<BITS> c;
+                    const int wr = slab * 32 * RS + 32 * rs + r;   // row within the tile
                     if constexpr (BITS == 8) {
                         const int sw = (r >> 2) & 3;
-                        const unsigned char *ra = base + (m + mw) * A_ST + (slab * 32 + r) * 64;
+                        const unsigned char *ra = base + (m + mw) * A_ST + wr * 64;
                         const u32x4 v0 = *reinterpret_cast<const u32x4 *>(ra + 16 * ((2 * h) ^ sw));
                         const u32x4 v1 = *reinterpret_cast<const u32x4 *>(ra + 16 * ((2 * h + 1) ^ sw));
                         c.w[0] = v0.x; c.w[1] = v0.y; c.w[2] = v0.z; c.w[3] = v0.w;
                         c.w[4] = v1.x; c.w[5] = v1.y; c.w[6] = v1.z; c.w[7] = v1.w;
                     } else {
-                        const uint32_t *ra = reinterpret_cast<const uint32_t *>(base + (m + mw) * A_ST) + (slab * 32 + r) * 10 + 5 * h;
+                        const uint32_t *ra = reinterpret_cast<const uint32_t *>(base + (m + mw) * A_ST) + wr * 10 + 5 * h;
 #pragma unroll
                         for (int k = 0; k < 5; k++) c.w[k] = ra[k];
                     }
-                    const uint32_t sbits = (win[m][0][u >> 1] >> (16 * (u & 1))) & 0xffffu;
-                    const uint32_t bbits = (win[m][1][u >> 1] >> (16 * (u & 1))) & 0xffffu;
-                    chunk_to_bf16<BITS>(c, bf16_to_f32(sbits), bf16_to_f32(bbits), a[m]);
+                    const uint32_t sbits = (win[rs][m][0][u >> 1] >> (16 * (u & 1))) & 0xffffu;
+                    const uint32_t bbits = (win[rs][m][1][u >> 1] >> (16 * (u & 1))) & 0xffffu;
+                    chunk_to_bf16<BITS>(c, bf16_to_f32(sbits), bf16_to_f32(bbits), a[rs * WMAT + m]);
                 }
                 // MFMAs over all NT route tiles
                 const unsigned char *bb = base + NMAT * A_ST;
@@ -557,7 +570,9 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
                     }
 #pragma unroll
                     for (int i = 0; i < NT; i++) {
-                        acc0[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][j], bx[i], acc0[i], 0, 0, 0);
+#pragma unroll
+                        for (int rs = 0; rs < RS; rs++)
+                            acc0[rs][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rs * WMAT][j], bx[i], acc0[rs][i], 0, 0, 0);
                         if constexpr (GATED && !SPLIT)
                             acc1[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][j], bx[i], acc1[i], 0, 0, 0);
                     }
@@ -565,7 +580,9 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
             }
             if (more) {
 #pragma unroll
-                for (int m = 0; m < WMAT; m++) { win[m][0] = win_next[m][0]; win[m][1] = win_next[m][1]; }
+                for (int rs = 0; rs < RS; rs++)
+#pragma unroll
+                    for (int m = 0; m < WMAT; m++) { win[rs][m][0] = win_next[rs][m][0]; win[rs][m][1] = win_next[rs][m][1]; }
             }
         }
 
@@ -578,13 +595,15 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
 #pragma unroll
                 for (int i = 0; i < NT; i++) {
 #pragma unroll
-                    for (int k = 0; k < 16; k++) xw[(i * 16 + k) * 64] = siluf_(acc0[i][k]);
+                    for (int k = 0; k < 16; k++) xw[(i * 16 + k) * 64] = siluf_(acc0[0][i][k]);
                 }
             }
             wait_lgkm0();
             barrier_no_fence();
         }
-        const int row_base = (rt0 + ti) * 128 + slab * 32;
+#pragma unroll
+        for (int rs = 0; rs < RS; rs++) {
+        const int row_base = (rt0 + ti) * TR + slab * 32 * RS + 32 * rs;
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             const int n = 32 * i + r;
@@ -596,7 +615,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
                 float v[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const float g = acc0[i][4 * q + k];
+                    const float g = acc0[rs][i][4 * q + k];
                     if constexpr (SPLIT) v[k] = xch[(slab * NT * 16 + i * 16 + 4 * q + k) * 64 + lane] * g;
                     else if constexpr (GATED) v[k] = siluf_(g) * acc1[i][4 * q + k];
                     else v[k] = g;
@@ -622,6 +641,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
                 }
             }
         }
+        }
         zero_acc();
     }
     // no copy may still be writing this block's LDS when the block exits
@@ -630,8 +650,8 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (qmm_lds_occupancy<BITS, GATED, 
 
 // Upper bound of (row tile, chunk) work items: sum_g ceil(count_g / BN) <= routes / BN +
 // (groups holding any route); a shared-expert group adds `tokens` routes.
-static size_t qmm_max_work(int rows, int tokens, int ngroups, int dense, int bn) {
-    const size_t row_tiles = (size_t)(rows + 127) / 128;
+static size_t qmm_max_work(int rows, int tokens, int ngroups, int dense, int bn, int tile_rows = 128) {
+    const size_t row_tiles = (size_t)(rows + tile_rows - 1) / tile_rows;
     if (dense) return row_tiles * ((size_t)(tokens + bn - 1) / bn);
     const size_t routes = (size_t)tokens * 9;
     return row_tiles * (routes / bn + std::min<size_t>((size_t)ngroups, routes));
@@ -667,7 +687,13 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     const bool streaming = m0->columns % 512 == 0;
     const int nt = streaming && !a.dense && !gated ? 2 : (gated ? 2 : 4);
     const int bn = 32 * nt;
-    const size_t work = qmm_max_work(m0->rows, a.tokens, a.ngroups, a.dense, bn);
+    // dense streaming GEMMs with enough (256-row tile, route chunk) items to fill the GPU:
+    // two 32-row slabs per wave (256-row tiles)
+    const bool two_slabs = streaming && a.dense && !gated &&
+                           (size_t)((m0->rows + 255) / 256) * (size_t)((a.tokens + bn - 1) / bn) >= 256;
+    const int tile_rows = two_slabs ? 256 : 128;
+    P.row_tiles = (m0->rows + tile_rows - 1) / tile_rows;
+    const size_t work = qmm_max_work(m0->rows, a.tokens, a.ngroups, a.dense, bn, tile_rows);
     const size_t blocks = 8 * ((work + 7) / 8);
     if (blocks == 0 || blocks > 0x7fffffffu) {
         set_error(error, capacity, "Invalid qmm grid");
@@ -693,14 +719,15 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         // 5-bit gated: the split eight-wave form (gate and up on different waves; its
         // costlier code extraction then overlaps the other wave's MFMAs: 6 % faster on
         // config 4, while 8-bit gated measured no gain)
-#define DIH_QMM_LDS_CASE(B, GT, N)                                                  \
-        if (m0->bits == B && gated == GT && nt == N) {                              \
+#define DIH_QMM_LDS_CASE(B, GT, N, R2)                                              \
+        if (m0->bits == B && gated == GT && nt == N && two_slabs == R2) {            \
             constexpr bool SP = GT && B == 5;                                       \
-            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP>), grid, dim3(SP ? 512 : 256), 0, s, P); \
+            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1>), grid, dim3(SP ? 512 : 256), 0, s, P); \
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }
-        DIH_QMM_LDS_CASE(8, true, 2) DIH_QMM_LDS_CASE(8, false, 2) DIH_QMM_LDS_CASE(8, false, 4)
-        DIH_QMM_LDS_CASE(5, true, 2) DIH_QMM_LDS_CASE(5, false, 2) DIH_QMM_LDS_CASE(5, false, 4)
+        DIH_QMM_LDS_CASE(8, true, 2, false) DIH_QMM_LDS_CASE(8, false, 2, false) DIH_QMM_LDS_CASE(8, false, 4, false)
+        DIH_QMM_LDS_CASE(5, true, 2, false) DIH_QMM_LDS_CASE(5, false, 2, false) DIH_QMM_LDS_CASE(5, false, 4, false)
+        DIH_QMM_LDS_CASE(8, false, 4, true) DIH_QMM_LDS_CASE(5, false, 4, true)
 #undef DIH_QMM_LDS_CASE
     }
 #define DIH_QMM_CASE(B, GT, N, D)                                                   \

@@ -400,6 +400,24 @@ def test_dense_matches_oracle(device, bits, rows, columns, T):
         m.dispose()
 
 
+@pytest.mark.parametrize("bits,rows,columns,T", [(8, 2048, 512, 4096), (5, 2000, 512, 4000)])
+def test_dense_two_slab_tiles(device, bits, rows, columns, T):
+    """Dense launches with at least 256 (256-row tile, 128-token chunk) items run 256-row
+    tiles, two 32-row slabs a wave; ragged rows and tokens included."""
+    rng = np.random.default_rng(rows + T)
+    host = orc.random_matrix(rng, 1, rows, columns, bits)
+    m = upload(device, host)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, columns)).astype(np.float32))
+        y = torch.zeros((T, rows), dtype=torch.float32, device="cuda")
+        dh.dense(device, m, T, dev_bf16(xb), y)
+        torch.cuda.synchronize()
+        want_bf = orc.dense_f64(host, orc.bf16_bits_to_f32(xb), round_operands=True)
+        assert orc.rel_err(y.cpu().numpy(), want_bf) < 1e-4
+    finally:
+        m.dispose()
+
+
 def test_bf16_dense_check_cases(device):
     """bf16_checks.mm:12-35: closed-form weights, amplitudes .2 and 1e10, relative L2 < 2e-5
     against bf16-rounded double products."""

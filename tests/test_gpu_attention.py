@@ -105,6 +105,39 @@ def test_attention_bf16_operands(device, inputs):
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + ABS_TOL)
 
 
+@pytest.mark.parametrize("position", [0, 31, 32, 96, 127, 128, 129, 255, 1000, 8191])
+def test_attention_decode_positions(device, inputs, position):
+    """One decode token (the decode kernel: 128-key blocks of four 32-key tiles) at block
+    and tile edges, where some of a block's tiles have no keys, and with cache rows past
+    the position set to NaN (they must not be read into the result)."""
+    I = inputs
+    k = I.dk.clone()
+    v = I.dv.clone()
+    k[position + 1:] = 0x7fc0   # bf16 NaN
+    v[position + 1:] = 0x7fc0
+    out = torch.full((1, 4096), float("nan"), device="cuda")
+    dh.attention(device, I.dq, k, v, I.draw, out, position, 1)
+    torch.cuda.synchronize()
+    assert dh.attention_partition(position, 1) == 32
+    want = orc.attention_f64(I.q[:1], I.k, I.v, I.raw[:1], position, partition=32)
+    _check(out.cpu().numpy(), want)
+
+
+def test_attention_decode_bf16(device, inputs):
+    """The decode kernel with bf16 queries, gate and output."""
+    I = inputs
+    position = 3000
+    qb = orc.round_bf16(I.q[:1])
+    rb = orc.round_bf16(I.raw[:1])
+    out = torch.zeros((1, 4096), dtype=torch.int16, device="cuda")
+    dh.attention(device, _bf16_dev(qb), I.dk, I.dv, _bf16_dev(rb), out, position, 1,
+                 q_dtype=dh.BF16, gate_dtype=dh.BF16, out_dtype=dh.BF16)
+    torch.cuda.synchronize()
+    got = orc.bf16_bits_to_f32(out.cpu().numpy().view(np.uint16)).astype(np.float64)
+    want = orc.attention_f64(qb, I.k, I.v, rb, position, partition=32)
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + ABS_TOL)
+
+
 def test_attention_matches_exact_softmax(device, inputs):
     """Against the plain double softmax of unrounded operands: the bf16 rounding of q and
     of the probabilities stays within a few bf16 ulps of the values' scale."""

@@ -169,7 +169,7 @@ def test_top8_flags_non_finite(device):
     assert list(ids.cpu().numpy()[0]) == list(range(8))
 
 
-@pytest.mark.parametrize("count", [64, 65, 127, 128, 129, 512, 513, 2048])
+@pytest.mark.parametrize("count", [1, 3, 64, 65, 127, 128, 129, 512, 513, 2048, 2049, 4100])
 @pytest.mark.parametrize("pattern", [0, 1, 2])
 def test_build_groups_is_bit_exact(device, count, pattern):
     """Route lists, counts and their invariants (prefill_expert_checks.mm:26-52)."""

@@ -264,7 +264,9 @@ int dih_attention(void *context, const void *q, int q_dtype, const uint16_t *key
 /* The partition size dih_attention uses for these arguments (`partition` itself when it
  * is positive, else the library's choice); -1 for invalid arguments. The partition sets
  * where probabilities are rounded (see dih_attention) and the partial-result scratch:
- * tokens * 16 * ceil((position + tokens) / partition) * 1032 bytes when above one. */
+ * tokens * 16 * ceil((position + tokens) / partition) * 1032 bytes when above one (one
+ * token with 32-key partitions: 16 * ceil((position + 1) / 128) * 1032 bytes, the decode
+ * kernel merging four partitions a block). */
 int dih_attention_partition(int position, int tokens, int partition);
 
 /* Gated delta rule of a linear-attention (Gated DeltaNet) layer over a chunk of `tokens`

@@ -949,7 +949,7 @@ __attribute__((visibility("default"))) int dih_attention(void *ctx, const void *
         return -1;
     }
     const int part = attention_partition(position, tokens, partition);
-    const size_t nparts = ((size_t)position + tokens + part - 1) / part;
+    const size_t nparts = (size_t)attention_partials(position, tokens, part);
     AttentionArgs a;
     a.q = q; a.q_bf16 = q_dtype == DIH_BF16;
     a.keys = keys; a.values = values;

@@ -733,6 +733,11 @@ int attention_partition(int position, int tokens, int requested) {
     return part < 256 ? 256 : part;
 }
 
+int attention_partials(int position, int tokens, int partition) {
+    if (tokens == 1 && partition == kKeys) return (position + kDecKeys) / kDecKeys;   // decode blocks
+    return (position + tokens + partition - 1) / partition;
+}
+
 bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity) {
     AttnParams P;
     P.q = a.q; P.q_bf16 = a.q_bf16;
@@ -741,7 +746,7 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
     P.out = a.out; P.out_bf16 = a.out_bf16;
     P.pacc = a.pacc; P.pstat = reinterpret_cast<float2 *>(a.pstat);
     P.position = a.position; P.tokens = a.tokens; P.partition = a.partition;
-    P.nparts = (a.position + a.tokens + a.partition - 1) / a.partition;
+    P.nparts = attention_partials(a.position, a.tokens, a.partition);
     const bool wide = wide_blocks(a.tokens);
     P.ntiles = (a.tokens + (wide ? 2 * kTok : kTok) - 1) / (wide ? 2 * kTok : kTok);
     if (P.nparts > 1 && (!P.pacc || !P.pstat)) {
@@ -752,11 +757,6 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
         // decode: four 32-key partitions a block, merged there; the blocks' partial results
         // are combined by (token, head, 32 dims)
         P.partition = kDecKeys;
-        P.nparts = (a.position + 1 + kDecKeys - 1) / kDecKeys;
-        if (P.nparts > 1 && (!P.pacc || !P.pstat)) {
-            set_error(error, capacity, "Attention partitions need partial buffers");
-            return false;
-        }
         prof_stage("attention");
         const dim3 grid(2 * ((P.nparts + 3) / 4 * 4));
         if (P.q_bf16)

@@ -215,6 +215,8 @@ struct AttentionArgs {
 // Partition size for a call: `requested` when positive, else enough partitions that the
 // blocks fill the GPU.
 int attention_partition(int position, int tokens, int requested);
+// Partial-result slots per (token, head) a call with that partition writes (1: none).
+int attention_partials(int position, int tokens, int partition);
 bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity);
 
 // Gated delta rule over a chunk (delta.hip): state [32][128][128] f32 and history

@@ -263,15 +263,19 @@ __global__ __launch_bounds__(256) void delta_prepare_kernel(DeltaParams P) {
             cs[at] = (qkp[0][at] + qkp[1][at]) * dd;
             lt[at] = t > j ? b[t] * dd * (kkp[0][at] + kkp[1][at]) : 0.f;
         }
-        // g_t = a_0..a_t and the tail a_{t+1}..a_{valid-1}, both as direct products
+        // g_t = a_0..a_t and the tail a_{t+1}..a_{valid-1}, both as direct products (no
+        // quotients), by prefix and suffix product scans over lanes 0..31
         if (tid < kBlk) {
             const int t = tid;
-            float p = 1.f, tail = 1.f;
+            float p = a[t], sfx = t < valid ? a[t] : 1.f;
 #pragma unroll
-            for (int k = 0; k < kBlk; k++) {
-                p *= k <= t ? ar[k] : 1.f;
-                tail *= k > t && k < valid ? ar[k] : 1.f;
+            for (int d = 1; d < kBlk; d <<= 1) {
+                const float up = __shfl_up(p, d, kBlk), down = __shfl_down(sfx, d, kBlk);
+                if (t >= d) p *= up;
+                if (t + d < kBlk) sfx *= down;
             }
+            float tail = __shfl_down(sfx, 1, kBlk);
+            if (t == kBlk - 1) tail = 1.f;
             bg[t] = b[t] * p;
             gs[t] = p;
             tl[t] = t < valid ? tail : 0.f;

@@ -548,13 +548,12 @@ __attribute__((visibility("default"))) int dih_argmax(void *ctx, const float *va
         set_error(error, capacity, "Invalid argmax arguments");
         return -1;
     }
-    const size_t parts = (size_t)(n + 1023) / 1024;
+    const size_t parts = (size_t)(n + kArgmaxPer - 1) / kArgmaxPer;
     float *pv = static_cast<float *>(scratch(c, S_ARGVAL, parts * 4, error, capacity));
     uint32_t *pi = static_cast<uint32_t *>(scratch(c, S_ARGIDX, parts * 4, error, capacity));
-    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
-    if (!pv || !pi || !tk) return -1;
+    if (!pv || !pi) return -1;
     hipStream_t s = pick(c, stream);
-    return launch_argmax(values, n, pv, pi, tk + 1, next, s, error, capacity) ? 0 : -1;
+    return launch_argmax(values, n, pv, pi, next, s, error, capacity) ? 0 : -1;
 }
 
 __attribute__((visibility("default"))) int dih_lm_head(void *ctx, void *const *slices, int slice_count,
@@ -581,11 +580,10 @@ __attribute__((visibility("default"))) int dih_lm_head(void *ctx, void *const *s
     }
     for (int i = 0; i < slice_count; i++)
         if (!sync_matrix(as_mat(slices[i]), error, capacity)) return -1;
-    const size_t parts = (size_t)(total + 1023) / 1024;
+    const size_t parts = (size_t)(total + kArgmaxPer - 1) / kArgmaxPer;
     float *pv = static_cast<float *>(scratch(c, S_ARGVAL, parts * 4, error, capacity));
     uint32_t *pi = static_cast<uint32_t *>(scratch(c, S_ARGIDX, parts * 4, error, capacity));
-    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
-    if (!pv || !pi || !tk) return -1;
+    if (!pv || !pi) return -1;
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);
     long offset = 0;
@@ -602,7 +600,7 @@ __attribute__((visibility("default"))) int dih_lm_head(void *ctx, void *const *s
         if (!launch_qmv(segs, n, first->bits, nullptr, s, error, capacity)) return -1;
     }
     prof_mark(c, s, "lm_head_qmv");
-    if (!launch_argmax(logits, (int)total, pv, pi, tk + 1, next, s, error, capacity)) return -1;
+    if (!launch_argmax(logits, (int)total, pv, pi, next, s, error, capacity)) return -1;
     prof_mark(c, s, "argmax");
     return 0;
 }
@@ -732,9 +730,8 @@ __attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const 
     float *sout = static_cast<float *>(scratch(c, S_SOUT, (size_t)H * 4, error, capacity));
     uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
     float *probs = static_cast<float *>(scratch(c, S_PROBS, 8 * 4, error, capacity));
-    uint32_t *tk = static_cast<uint32_t *>(scratch(c, S_TICKETS, 64, error, capacity));
     uint32_t *status = static_cast<uint32_t *>(scratch(c, S_STATUS, 16, error, capacity));
-    if (!lg || !srt || !sact || !act || !sout || !ids || !probs || !tk || !status) return -1;
+    if (!lg || !srt || !sact || !act || !sout || !ids || !probs || !status) return -1;
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);
     if (decode_fast_path_ok(router, gate, down, sg, sd, sr)) {
@@ -769,7 +766,6 @@ __attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const 
     int n8 = 0;
     Top8Source tp;
     tp.logits = use_logits; tp.experts = E; tp.ids = ids; tp.probs = probs; tp.status = trace ? trace->status : nullptr;
-    (void)tk;
     if (router) {
         QmvSeg a = seg_of(router);
         a.x = x; a.x_bf16 = 1; a.y = lg;

@@ -58,7 +58,7 @@ struct Context {
 };
 
 enum ScratchId {
-    S_IDS, S_PROBS, S_STATUS, S_TICKETS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
+    S_IDS, S_PROBS, S_STATUS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
     S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_COUNT_
 };
@@ -192,8 +192,9 @@ bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix 
                          const Matrix *sd, const Matrix *sr);
 bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int capacity);
 
+constexpr int kArgmaxPer = 4096;   // values per first-level argmax block (partials per call)
 bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
-                   uint32_t *ticket, uint32_t *next, hipStream_t s, char *error, int capacity);
+                   uint32_t *next, hipStream_t s, char *error, int capacity);
 
 bool launch_dequant_bf16(const Matrix *m, int expert, uint16_t *out, hipStream_t s, char *error,
                          int capacity);

@@ -250,82 +250,98 @@ bool launch_rmsnorm(const void *r, int r_f32, int tokens, int hidden, const floa
 
 // --------------------------------------------------------------------------- argmax
 
-// Two levels in one launch (graph_argmax_blocks/final gpu_graph.mm:160-175): each block
-// reduces 1024 values to (max, lowest index), flagging non-finite values; the last block
-// to finish reduces the partials. Result 0xffffffff when any value is not finite.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *v, int n, float *pval,
-                                                     uint32_t *pidx, uint32_t *ticket,
-                                                     uint32_t *next) {
-    __shared__ float wv[4];
-    __shared__ uint32_t wi[4];
-    __shared__ int last;
+// Two levels, two launches (graph_argmax_blocks/final gpu_graph.mm:160-175): each block of
+// the first reduces 4096 values to (max, lowest index), flagging non-finite values; one block
+// of the second reduces the partials. Result 0xffffffff when any value is not finite. (One
+// launch with a last-block ticket measured 10.7-12 us: the ticket's release fence and
+// device-scope atomic from every block cost more than the second launch.)
+
+// (max, lowest index) of a block's candidates; pairs whose index is 0xfffffffe mark a
+// non-finite value, and 0xffffffff marks "no candidate". Thread 0 gets the result.
+DIH_DEV void argmax_block(float best, uint32_t id, bool bad, float *wv, uint32_t *wi,
+                          float &bm, uint32_t &bi) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float best = -INFINITY;
-    uint32_t id = 0xffffffffu;
-    bool bad = false;
-    const int base = blockIdx.x * 1024;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int at = base + k * 256 + tid;
-        if (at < n) {
-            const float x = v[at];
-            if (!isfinite(x)) bad = true;
-            else if (x > best || (x == best && (uint32_t)at < id)) { best = x; id = (uint32_t)at; }
-        }
-    }
     const bool any_bad_w = __any(bad);
-    float m = wave_max(best);
-    uint32_t sel = wave_min_u32(best == m ? id : 0xffffffffu);
+    const float m = wave_max(best);
+    const uint32_t sel = wave_min_u32(best == m ? id : 0xffffffffu);
     if (lane == 0) { wv[wave] = m; wi[wave] = any_bad_w ? 0xfffffffeu : sel; }
     __syncthreads();
+    bm = -INFINITY;
+    bi = 0xffffffffu;
     if (tid == 0) {
-        float bm = wv[0];
-        uint32_t bi = wi[0];
-        bool invalid = wi[0] == 0xfffffffeu;
-        for (int w = 1; w < 4; w++) {
-            if (wi[w] == 0xfffffffeu) { invalid = true; continue; }
-            if (wv[w] > bm || (wv[w] == bm && wi[w] < bi) || bi == 0xfffffffeu) { bm = wv[w]; bi = wi[w]; }
-        }
-        pval[blockIdx.x] = bm;
-        pidx[blockIdx.x] = invalid ? 0xfffffffeu : bi;
-        __threadfence();
-        last = (atomicAdd(ticket, 1u) == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    float b2 = -INFINITY;
-    uint32_t i2 = 0xffffffffu;
-    bool bad2 = false;
-    for (int k = tid; k < (int)gridDim.x; k += 256) {
-        const uint32_t pi = pidx[k];
-        const float pv = pval[k];
-        if (pi == 0xfffffffeu) bad2 = true;
-        else if (pi != 0xffffffffu && (pv > b2 || (pv == b2 && pi < i2))) { b2 = pv; i2 = pi; }
-    }
-    const bool bad_w = __any(bad2);
-    float m2 = wave_max(b2);
-    uint32_t s2 = wave_min_u32(b2 == m2 ? i2 : 0xffffffffu);
-    if (lane == 0) { wv[wave] = m2; wi[wave] = bad_w ? 0xfffffffeu : s2; }
-    __syncthreads();
-    if (tid == 0) {
-        float bm = -INFINITY;
-        uint32_t bi = 0xffffffffu;
         bool invalid = false;
         for (int w = 0; w < 4; w++) {
             if (wi[w] == 0xfffffffeu) { invalid = true; continue; }
             if (wi[w] != 0xffffffffu && (wv[w] > bm || (wv[w] == bm && wi[w] < bi))) { bm = wv[w]; bi = wi[w]; }
         }
-        *next = invalid ? 0xffffffffu : bi;
-        *ticket = 0u;
+        if (invalid) bi = 0xfffffffeu;
     }
 }
 
+__global__ __launch_bounds__(256) void argmax_blocks_kernel(const float *v, int n, float *pval,
+                                                            uint32_t *pidx) {
+    __shared__ float wv[4];
+    __shared__ uint32_t wi[4];
+    const int tid = threadIdx.x;
+    const int base = blockIdx.x * kArgmaxPer;
+    float x[16];
+    // four coalesced 16-byte loads a thread when the block is whole and aligned, else scalar
+    if (base + kArgmaxPer <= n && (reinterpret_cast<uintptr_t>(v) & 15) == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 q = *reinterpret_cast<const float4 *>(v + base + 1024 * k + 4 * tid);
+            x[4 * k] = q.x; x[4 * k + 1] = q.y; x[4 * k + 2] = q.z; x[4 * k + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int at = base + 1024 * (k >> 2) + 4 * tid + (k & 3);
+            x[k] = at < n ? v[at] : -INFINITY;
+        }
+    }
+    float best = -INFINITY;
+    uint32_t id = 0xffffffffu;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int at = base + 1024 * (k >> 2) + 4 * tid + (k & 3);
+        if (at < n) {
+            if (!isfinite(x[k])) bad = true;
+            else if (x[k] > best || (x[k] == best && (uint32_t)at < id)) { best = x[k]; id = (uint32_t)at; }
+        }
+    }
+    float bm;
+    uint32_t bi;
+    argmax_block(best, id, bad, wv, wi, bm, bi);
+    if (tid == 0) { pval[blockIdx.x] = bm; pidx[blockIdx.x] = bi; }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float *pval, const uint32_t *pidx,
+                                                           int nparts, uint32_t *next) {
+    __shared__ float wv[4];
+    __shared__ uint32_t wi[4];
+    float best = -INFINITY;
+    uint32_t id = 0xffffffffu;
+    bool bad = false;
+    for (int k = threadIdx.x; k < nparts; k += 256) {
+        const uint32_t pi = pidx[k];
+        const float pv = pval[k];
+        if (pi == 0xfffffffeu) bad = true;
+        else if (pi != 0xffffffffu && (pv > best || (pv == best && pi < id))) { best = pv; id = pi; }
+    }
+    float bm;
+    uint32_t bi;
+    argmax_block(best, id, bad, wv, wi, bm, bi);
+    if (threadIdx.x == 0) *next = bi == 0xfffffffeu ? 0xffffffffu : bi;
+}
+
 bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
-                   uint32_t *ticket, uint32_t *next, hipStream_t s, char *error, int capacity) {
-    const int blocks = (n + 1023) / 1024;
-    DIH_LAUNCH(argmax_kernel, dim3(blocks), dim3(256), 0, s, values, n, part_val, part_idx,
-                       ticket, next);
+                   uint32_t *next, hipStream_t s, char *error, int capacity) {
+    static_assert(kArgmaxPer == 16 * 256, "16 values a thread");
+    const int blocks = (n + kArgmaxPer - 1) / kArgmaxPer;
+    DIH_LAUNCH(argmax_blocks_kernel, dim3(blocks), dim3(256), 0, s, values, n, part_val, part_idx);
+    if (!hip_ok(hipGetLastError(), error, capacity, "argmax launch")) return false;
+    DIH_LAUNCH(argmax_final_kernel, dim3(1), dim3(256), 0, s, part_val, part_idx, blocks, next);
     return hip_ok(hipGetLastError(), error, capacity, "argmax launch");
 }
 

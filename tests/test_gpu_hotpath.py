@@ -238,6 +238,25 @@ def test_argmax_known_answers(device):
         assert orc.argmax(v) == want
 
 
+def test_argmax_block_edges(device):
+    """Ties across the 4096-value first-level blocks, a maximum in a partial last block,
+    and values that start off 16-byte alignment (the scalar load path)."""
+    cases = []
+    t = np.full(12289, -3, dtype=np.float32); t[4095] = t[4096] = 2; cases.append((t, 4095, 0))
+    t = np.full(12289, -3, dtype=np.float32); t[12288] = 5; cases.append((t, 12288, 0))
+    t = np.full(12289, -3, dtype=np.float32); t[8191] = t[8192] = t[12000] = 4; cases.append((t, 8191, 0))
+    t = np.full(8193, -3, dtype=np.float32); t[7] = 1; t[4100] = 1; cases.append((t, 7, 1))
+    t = np.full(8193, -3, dtype=np.float32); t[8000] = np.nan; cases.append((t, 0xFFFFFFFF, 3))
+    for v, want, shift in cases:
+        buf = torch.full((v.size + shift,), 99.0, device="cuda")
+        buf[shift:] = torch.from_numpy(v).cuda()
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        dh.argmax(device, buf[shift:], v.size, nxt)
+        torch.cuda.synchronize()
+        assert int(u32(nxt)[0]) == want, (v.size, shift)
+        assert orc.argmax(v) == want
+
+
 # ------------------------------------------------------------------------------- MoE
 
 def _moe_layer(rng, E, H, I, bits, router=True):

@@ -350,7 +350,9 @@ def _zipf_logits(rng, T, E, s=1.1):
 @pytest.mark.parametrize("T,E,H,I,bits,routing", [
     (64, 32, 256, 128, 8, "zipf"), (65, 32, 256, 128, 5, "uniform"), (200, 256, 512, 128, 8, "zipf"),
     (129, 16, 128, 192, 5, "uniform"), (1, 16, 128, 64, 8, "uniform"),
-    (96, 64, 1024, 512, 5, "zipf")])   # 5-bit with K multiples of 512: the streaming kernels
+    (96, 64, 1024, 512, 5, "zipf"),    # 5-bit with K multiples of 512: the streaming kernels
+    (96, 64, 1024, 512, 8, "zipf"),    # 8-bit streaming gate/up at K=1024 and down at K=512
+    (320, 64, 512, 512, 5, "uniform"), (300, 64, 512, 512, 8, "zipf")])
 def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
     rng = np.random.default_rng(T * 7 + E)
     L = _moe_layer(rng, E, H, I, bits, router=False)

@@ -646,15 +646,20 @@ __global__ __launch_bounds__(256) void attn_combine_wide_kernel(AttnParams P) {
     const int np = (P.position + tok) / P.partition + 1;
     const size_t pi = (size_t)th * P.nparts;
     const float2 *st = P.pstat + pi;
-    // eight of the group's partitions at a time, their loads issued together
+    // eight of the group's partitions at a time, their loads issued together. Up to 256
+    // partitions (32K keys) the partial rows are loaded with the statistics, before the
+    // maximum is known: one global round trip instead of two.
     constexpr int U = 8;
+    const bool one = np <= 32 * U;
     float m = -INFINITY;
     float2 sv[U];
+    float4 av[U];
     for (int p0 = pg; p0 < np; p0 += 32 * U) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int p = p0 + 32 * u;
-            sv[u] = st[min(p, np - 1)];
+            const int p = min(p0 + 32 * u, np - 1);
+            sv[u] = st[p];
+            if (one) av[u] = *reinterpret_cast<const float4 *>(P.pacc + (pi + p) * kDim + d0);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) m = fmaxf(m, sv[u].x);
@@ -665,8 +670,15 @@ __global__ __launch_bounds__(256) void attn_combine_wide_kernel(AttnParams P) {
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     float total = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int p0 = pg; p0 < np; p0 += 32 * U) {
-        float4 av[U];
+    if (one && pg < np) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float w = pg + 32 * u < np ? exp2f(sv[u].x - m) : 0.f;
+            total += w * sv[u].y;
+            acc.x += w * av[u].x; acc.y += w * av[u].y; acc.z += w * av[u].z; acc.w += w * av[u].w;
+        }
+    }
+    for (int p0 = one ? np : pg; p0 < np; p0 += 32 * U) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int p = min(p0 + 32 * u, np - 1);

@@ -123,6 +123,18 @@ def test_attention_decode_positions(device, inputs, position):
     _check(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("position", [32767, 32768, 40000])
+def test_attention_decode_long(device, position):
+    """One decode token past 32K keys: 256, 257 and 313 block partials per head, the last
+    two more than the wide combine loads in one round (its looped path)."""
+    I = Inputs(1, position + 1)
+    out = torch.full((1, 4096), float("nan"), device="cuda")
+    dh.attention(device, I.dq, I.dk, I.dv, I.draw, out, position, 1)
+    torch.cuda.synchronize()
+    want = orc.attention_f64(I.q[:1], I.k, I.v, I.raw[:1], position, partition=32)
+    _check(out.cpu().numpy(), want)
+
+
 def test_attention_decode_bf16(device, inputs):
     """The decode kernel with bf16 queries, gate and output."""
     I = inputs

@@ -17,6 +17,9 @@
  *   - Entry points whose name does not start with dih_quant_ take DEVICE pointers and a
  *     hipStream_t passed as void* (NULL = the context's own stream). They only enqueue
  *     work; the caller synchronizes the stream. bf16 buffers are raw uint16 bit patterns.
+ *     The context's stream is a blocking stream: work on it is ordered against the HIP
+ *     null stream in both directions (the legacy default-stream rule), so buffers a caller
+ *     fills on the null stream are complete before a NULL-stream call reads them.
  *   - Entry points named dih_quant_* take HOST pointers and are synchronous, like the
  *     reference's di_quant_* functions.
  *   - A context is single-stream and has no internal locking: callers serialize calls on
@@ -44,7 +47,7 @@ typedef struct dih_job {
 /* ---- context ------------------------------------------------------------------- */
 
 /* Replaces di_quant_create (quantized.mm:287-292). Uses device 0 of the process's
- * visible HIP devices and creates one non-blocking stream. */
+ * visible HIP devices and creates one blocking stream (ordered against the null stream). */
 void *dih_quant_create(char *error, int capacity);
 /* Replaces di_quant_create_configured (quantized.mm:245-286). `resident` (0/1) and
  * `refresh` (0..60000 ms) are validated like the reference; HIP device memory needs no
@@ -289,6 +292,23 @@ int dih_attention_partition(int position, int tokens, int partition);
 int dih_delta_rule(void *context, float *state, float *history, const float *conv,
                    const float *decay, const float *beta, const float *raw, float *out,
                    int tokens, int path, void *stream, char *error, int capacity);
+
+/* ---- host-pointer gated delta step (DeltaMemory) ----------------------------------- */
+
+/* Replaces di_delta_create (quantized.mm:398-406): a device-resident recurrent state
+ * f32 [32][128][128], zeroed, owned by `context`; NULL on failure. */
+void *dih_delta_create(void *context);
+/* Replaces di_delta_destroy (quantized.mm:407). */
+void dih_delta_destroy(void *state);
+/* Replaces di_delta_step (quantized.mm:408-423): one token of the gated delta rule
+ * (the dih_delta_rule recurrence without the history roll) on HOST pointers, synchronous:
+ *   q, k f32 [16][128] (key heads), v f32 [32][128], decay, beta f32 [32], out f32 [4096].
+ * For value head h and row r (key head h/2): S *= decay[h]; c = (v[h][r] - S.k) * beta[h];
+ * S += c k; out[h*128+r] = S.q. `ms` receives the GPU time of the step. Returns 0, or -1
+ * with "Null delta argument" when a pointer is NULL (nothing is launched then). */
+int dih_delta_step(void *context, void *state, const float *q, const float *k, const float *v,
+                   const float *decay, const float *beta, float *out, double *ms, char *error,
+                   int capacity);
 
 /* Per-stage GPU timing (the reference's DEEPINFER_METAL_GPU_PROFILE per-dispatch
  * timestamps, gpu_graph.mm:329-338, as a runtime switch instead of getenv). While enabled,

@@ -105,6 +105,10 @@ static Matrix *as_mat(void *p) {
     auto *m = static_cast<Matrix *>(p);
     return m && m->magic == 0x44494d58u ? m : nullptr;
 }
+// NULL selects the context's stream. That stream is a blocking one (hipStreamDefault), so
+// its work is ordered after everything queued earlier on the null stream (torch's default
+// stream) and before anything queued there later: a caller filling buffers on the null
+// stream and then calling a dih_* entry point with stream NULL needs no synchronization.
 static hipStream_t pick(Context *c, void *stream) {
     return stream ? static_cast<hipStream_t>(stream) : c->stream;
 }
@@ -173,7 +177,7 @@ __attribute__((visibility("default"))) void *dih_quant_create_configured(int res
     }
     c->device = dev;
     c->resident = resident == 1;
-    if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), error, capacity, "stream") ||
+    if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamDefault), error, capacity, "stream") ||
         !hip_ok(hipEventCreate(&c->start), error, capacity, "event") ||
         !hip_ok(hipEventCreate(&c->stop), error, capacity, "event")) {
         delete c;
@@ -997,6 +1001,100 @@ __attribute__((visibility("default"))) int dih_delta_rule(void *ctx, float *stat
     bool ok = launch_delta_rule(a, s, error, capacity);
     prof_mark(c, s, "delta");
     return ok ? 0 : -1;
+}
+
+// ---------------------------------------------------------------- host-pointer delta step
+
+namespace dih {
+// Device memory of one DeltaMemory (DeltaState, quantized.mm:21-23): the recurrent state
+// and the staging of one token's operands, in one allocation.
+struct DeltaState {
+    Context *ctx = nullptr;
+    float *block = nullptr;
+    uint32_t magic = 0x44494453u;
+    static constexpr size_t kState = 32 * 128 * 128, kConv = 8192, kHeads = 32, kOut = 4096;
+    static constexpr size_t kHistory = 3 * 8192;
+    static constexpr size_t kFloats = kState + kConv + 2 * kHeads + kOut + kHistory;
+    float *state() const { return block; }
+    float *conv() const { return block + kState; }          // q [2048], k [2048], v [4096]
+    float *decay() const { return conv() + kConv; }
+    float *beta() const { return decay() + kHeads; }
+    float *out() const { return beta() + kHeads; }
+    float *history() const { return out() + kOut; }         // unused roll target of the kernel
+};
+static DeltaState *as_delta(void *p) {
+    auto *d = static_cast<DeltaState *>(p);
+    return d && d->magic == 0x44494453u ? d : nullptr;
+}
+}  // namespace dih
+
+__attribute__((visibility("default"))) void *dih_delta_create(void *ctx) {
+    Context *c = as_ctx(ctx);
+    if (!c) return nullptr;
+    auto *d = new (std::nothrow) DeltaState();
+    if (!d) return nullptr;
+    d->ctx = c;
+    if (hipMalloc(&d->block, DeltaState::kFloats * 4) != hipSuccess) {
+        delete d;
+        return nullptr;
+    }
+    // the state starts at zero (di_delta_create memsets it); the rest is zeroed as well so
+    // that the kernel's history roll never reads uninitialized memory
+    if (hipMemset(d->block, 0, DeltaState::kFloats * 4) != hipSuccess) {
+        (void)hipFree(d->block);
+        delete d;
+        return nullptr;
+    }
+    return d;
+}
+
+__attribute__((visibility("default"))) void dih_delta_destroy(void *state) {
+    DeltaState *d = as_delta(state);
+    if (!d) return;
+    (void)hipStreamSynchronize(d->ctx->stream);
+    (void)hipFree(d->block);
+    d->magic = 0;
+    delete d;
+}
+
+__attribute__((visibility("default"))) int dih_delta_step(void *ctx, void *state, const float *q, const float *k,
+                                                          const float *v, const float *decay, const float *beta,
+                                                          float *out, double *ms, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    DeltaState *d = as_delta(state);
+    if (!c || !d || !q || !k || !v || !decay || !beta || !out) {
+        set_error(error, capacity, "Null delta argument");
+        return -1;
+    }
+    if (d->ctx != c) {
+        set_error(error, capacity, "Delta state belongs to another context");
+        return -1;
+    }
+    hipStream_t s = c->stream;
+    if (!hip_ok(hipMemcpyAsync(d->conv(), q, 2048 * 4, hipMemcpyHostToDevice, s), error, capacity, "delta upload") ||
+        !hip_ok(hipMemcpyAsync(d->conv() + 2048, k, 2048 * 4, hipMemcpyHostToDevice, s), error, capacity,
+                "delta upload") ||
+        !hip_ok(hipMemcpyAsync(d->conv() + 4096, v, 4096 * 4, hipMemcpyHostToDevice, s), error, capacity,
+                "delta upload") ||
+        !hip_ok(hipMemcpyAsync(d->decay(), decay, 32 * 4, hipMemcpyHostToDevice, s), error, capacity,
+                "delta upload") ||
+        !hip_ok(hipMemcpyAsync(d->beta(), beta, 32 * 4, hipMemcpyHostToDevice, s), error, capacity, "delta upload"))
+        return -1;
+    // one token of the sequential delta rule (delta_step, quantized.mm:191-212, is the same
+    // recurrence); the raw rows of the history roll are the operands themselves
+    DeltaArgs a;
+    a.conv = d->conv(); a.decay = d->decay(); a.beta = d->beta(); a.raw = d->conv();
+    a.state = d->state(); a.history = d->history(); a.out = d->out(); a.tokens = 1; a.chunked = 0;
+    (void)hipEventRecord(c->start, s);
+    if (!launch_delta_rule(a, s, error, capacity)) return -1;
+    (void)hipEventRecord(c->stop, s);
+    if (!hip_ok(hipStreamSynchronize(s), error, capacity, "Gated delta HIP command failed")) return -1;
+    float elapsed = 0;
+    (void)hipEventElapsedTime(&elapsed, c->start, c->stop);
+    if (ms) *ms = elapsed;
+    return hip_ok(hipMemcpy(out, d->out(), 4096 * 4, hipMemcpyDeviceToHost), error, capacity, "delta download")
+               ? 0
+               : -1;
 }
 
 __attribute__((visibility("default"))) int dih_attention_partition(int position, int tokens, int partition) {

@@ -84,7 +84,8 @@ EXPORTS = [
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
     "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm",
     "dih_moe_prefill_norm", "dih_dense", "dih_attention",
-    "dih_attention_partition", "dih_delta_rule", "dih_set_profiling",
+    "dih_attention_partition", "dih_delta_rule", "dih_delta_create", "dih_delta_destroy",
+    "dih_delta_step", "dih_set_profiling",
     "dih_profile_read", "dih_version",
     "dih_safetensors_open", "dih_safetensors_close", "dih_safetensors_count",
     "dih_safetensors_info", "dih_safetensors_get", "dih_safetensors_read",
@@ -139,6 +140,9 @@ def load():
         "dih_attention": ([P, P, I, P, P, I, P, I, P, I, I, I, I, P, E, I], I),
         "dih_attention_partition": ([I, I, I], I),
         "dih_delta_rule": ([P, P, P, P, P, P, P, P, I, I, P, E, I], I),
+        "dih_delta_create": ([P], P),
+        "dih_delta_destroy": ([P], None),
+        "dih_delta_step": ([P, P, P, P, P, P, P, P, P, E, I], I),
         "dih_set_profiling": ([P, I], I),
         "dih_profile_read": ([P, P, P, P, I], I),
         "dih_version": ([], ctypes.c_char_p),
@@ -187,6 +191,9 @@ def _dp(t) -> Optional[int]:
 
 
 def _stream(stream) -> Optional[int]:
+    """The stream handle to pass: an explicit stream, else torch's current stream. Torch's
+    default stream is the HIP null stream (handle 0): it goes as NULL, which selects the
+    context's blocking stream, ordered against the null stream in both directions."""
     if stream is not None:
         return stream if isinstance(stream, int) else stream.cuda_stream
     try:
@@ -245,6 +252,14 @@ class QuantizedHip:
         if not p:
             raise InvalidOperationError(_msg(err))
         return QuantMatrix(self, p, experts, rows, columns, bits)
+
+    def new_delta_memory(self) -> "DeltaMemory":
+        """QuantizedMetal.NewDeltaMemory (QuantizedMetal.cs:47-52)."""
+        self._alive()
+        p = self._lib.dih_delta_create(self.context)
+        if not p:
+            raise InvalidOperationError("Cannot allocate gated-delta state.")
+        return DeltaMemory(self, p)
 
     def multiply_batch(self, jobs: Sequence["QuantizedJob"]) -> None:
         """QuantizedMetal.MultiplyBatch (QuantizedMetal.cs:54-112): 1..8 independent jobs."""
@@ -437,6 +452,37 @@ class QuantMatrix:
     def dispose(self) -> None:
         if self.handle is not None:
             self.owner._lib.dih_quant_matrix_destroy(self.handle)
+            self.handle = None
+
+
+class DeltaMemory:
+    """Mirror of ``DeltaMemory`` (QuantizedMetal.cs:207-225): one linear-attention layer's
+    recurrent state on the device, stepped one token at a time from host arrays."""
+
+    def __init__(self, owner: QuantizedHip, handle):
+        self.owner, self.handle = owner, handle
+
+    def step(self, q, k, v, decay, beta, output) -> None:
+        """DeltaMemory.Step (QuantizedMetal.cs:212-225)."""
+        if self.handle is None or self.owner.context is None:
+            raise ObjectDisposedError("DeltaMemory")
+        if (len(q) != 2048 or len(k) != 2048 or len(v) != 4096 or len(decay) != 32 or len(beta) != 32
+                or len(output) != 4096):
+            raise ArgumentError("Unsupported gated-delta dimensions.")
+        qa, ka, va, ga, ba = (_f32_in(a) for a in (q, k, v, decay, beta))
+        y = _f32_out(output)
+        err = _errbuf()
+        ms = ctypes.c_double()
+        rc = self.owner._lib.dih_delta_step(self.owner.context, self.handle, qa.ctypes.data, ka.ctypes.data,
+                                            va.ctypes.data, ga.ctypes.data, ba.ctypes.data, y.ctypes.data,
+                                            ctypes.byref(ms), err, _ERR)
+        _check(rc, err)
+        _copy_back(y, output)
+        self.owner.count(ms.value)
+
+    def dispose(self) -> None:
+        if self.handle is not None:
+            self.owner._lib.dih_delta_destroy(self.handle)
             self.handle = None
 
 

@@ -46,34 +46,34 @@ typedef struct dih_job {
 
 /* ---- context ------------------------------------------------------------------- */
 
-/* Replaces di_quant_create (quantized.mm:287-292). Uses device 0 of the process's
+/* Replaces di_quant_create (quantized.mm:282-286). Uses device 0 of the process's
  * visible HIP devices and creates one blocking stream (ordered against the null stream). */
 void *dih_quant_create(char *error, int capacity);
-/* Replaces di_quant_create_configured (quantized.mm:245-286). `resident` (0/1) and
+/* Replaces di_quant_create_configured (quantized.mm:242-281). `resident` (0/1) and
  * `refresh` (0..60000 ms) are validated like the reference; HIP device memory needs no
  * residency set, so `resident` only switches dih_quant_residency_bytes reporting on. */
 void *dih_quant_create_configured(int resident, int refresh, char *error, int capacity);
-/* Replaces di_quant_destroy (quantized.mm:299). Frees every scratch buffer. */
+/* Replaces di_quant_destroy (quantized.mm:293). Frees every scratch buffer. */
 void dih_quant_destroy(void *context);
-/* Replaces di_quant_residency_bytes (quantized.mm:293-295): device bytes held by the
+/* Replaces di_quant_residency_bytes (quantized.mm:287-289): device bytes held by the
  * weights of live matrices when created with resident=1, else 0. */
 uint64_t dih_quant_residency_bytes(void *context);
-/* Replaces di_quant_residency_prepare (quantized.mm:296-298). No work on HIP. */
+/* Replaces di_quant_residency_prepare (quantized.mm:290-292). No work on HIP. */
 void dih_quant_residency_prepare(void *context);
 
 /* ---- matrices -------------------------------------------------------------------- */
 
-/* Replaces di_quant_matrix_create (quantized.mm:300-320). Checks 1<=experts<=256,
+/* Replaces di_quant_matrix_create (quantized.mm:294-315). Checks 1<=experts<=256,
  * rows>=1, columns a multiple of 64 (at most 8192), bits 5 or 8, group 64. */
 void *dih_quant_matrix_create(void *context, int experts, int rows, int columns, int bits,
                               int group, char *error, int capacity);
-/* Replaces di_quant_matrix_buffer (quantized.mm:321-324). index 0 packed, 1 scales,
+/* Replaces di_quant_matrix_buffer (quantized.mm:316-319). index 0 packed, 1 scales,
  * 2 biases. Metal returns unified memory; here the pointer is a pinned HOST staging
  * copy of that buffer. Asking for the pointer marks the buffer dirty and the next call
  * that reads the matrix uploads it, so `write through the pointer, then multiply`
  * (QuantizedMetal.cs:171-178) works unchanged. NULL on a bad index. */
 void *dih_quant_matrix_buffer(void *matrix, int index);
-/* Replaces di_quant_matrix_destroy (quantized.mm:325). */
+/* Replaces di_quant_matrix_destroy (quantized.mm:320). */
 void dih_quant_matrix_destroy(void *matrix);
 
 /* New (HIP has no unified memory): copies `bytes` from `source` (host or device memory)
@@ -91,16 +91,16 @@ int dih_quant_matrix_shape(void *matrix, int *experts, int *rows, int *columns, 
 
 /* ---- synchronous host-pointer compute (reference ABI) ---------------------------- */
 
-/* Replaces di_quant_batch (quantized.mm:326-352): 1..8 jobs with distinct matrices;
+/* Replaces di_quant_batch (quantized.mm:321-345): 1..8 jobs with distinct matrices;
  * y[slot*rows+row] = sum_c w(experts[slot],row,c) * x[(batched?slot*columns:0)+c].
  * `ms` receives the GPU interval of the submission. */
 int dih_quant_batch(void *context, const dih_job *jobs, int count, double *ms, char *error,
                     int capacity);
-/* Replaces di_quant_matvec (quantized.mm:353-356). */
+/* Replaces di_quant_matvec (quantized.mm:346-349). */
 int dih_quant_matvec(void *context, void *matrix, const float *x, float *out,
                      const uint32_t *experts, int count, int batched, double *ms, char *error,
                      int capacity);
-/* Replaces di_quant_experts (quantized.mm:357-383): per slot, act = silu(gate.x)*(up.x),
+/* Replaces di_quant_experts (quantized.mm:350-383): per slot, act = silu(gate.x)*(up.x),
  * out[slot] = down[expert].act; sharedOut = shared.sharedInput. Three kernels, one
  * submission. */
 int dih_quant_experts(void *context, void *gate, void *up, void *down, void *shared,
@@ -233,6 +233,21 @@ int dih_moe_prefill_norm(void *context, const dih_moe_layer *layer, int tokens, 
                          const void *logits, int logits_dtype, void *residual,
                          const dih_moe_merge *merge, const dih_moe_trace *trace, void *stream,
                          char *error, int capacity);
+
+/* One grouped expert projection of prefill: the grouped gate/up (p_gate,
+ * gpu_prefill.mm:621-633) or the grouped down (p_gemv with experts, gpu_prefill.mm:603-620)
+ * on its own, over route lists from dih_build_groups. For every expert e and route
+ * r = routes[e*tokens + k], k < counts[e]:
+ *   up_matrix NULL:  y[r][row] = W[e][row] . x_in(r)
+ *   up_matrix set:   y[r][row] = silu(g) * u, g = W[e][row] . x_in(r), u = U[e][row] . x_in(r)
+ * with x_in(r) = x[r / 8] for input_mode 1 (the token's row: gate/up) and x[r] for
+ * input_mode 0 (the route's own row: down). bf16 operands (weights dequantized and rounded
+ * RNE), f32 accumulation; y f32 or bf16 [tokens*8][rows], rows of routes not listed are
+ * left unchanged. x bf16 [tokens or tokens*8][columns]; counts u32 [experts], routes u32
+ * [experts*tokens] (device). */
+int dih_grouped_qmm(void *context, void *matrix, void *up_matrix, int tokens, const void *x,
+                    int input_mode, const uint32_t *counts, const uint32_t *routes, void *y,
+                    int y_dtype, void *stream, char *error, int capacity);
 
 /* Dense batched projection through the same MFMA qmm (p_gemv dense path,
  * gpu_prefill.mm:603-614, prefill_bf16.mm:7-53): Y[t][r] = sum_c w(0,r,c)*X[t][c],

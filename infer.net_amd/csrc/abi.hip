@@ -902,6 +902,33 @@ __attribute__((visibility("default"))) int dih_moe_prefill_norm(void *ctx, const
     return 0;
 }
 
+__attribute__((visibility("default"))) int dih_grouped_qmm(void *ctx, void *matrix, void *up_matrix, int tokens,
+                                                           const void *x, int input_mode, const uint32_t *counts,
+                                                           const uint32_t *routes, void *y, int y_dtype,
+                                                           void *stream, char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    Matrix *m = as_mat(matrix), *up = up_matrix ? as_mat(up_matrix) : nullptr;
+    if (!c || !m || m->ctx != c || (up_matrix && (!up || up->ctx != c || up == m)) || tokens < 1 ||
+        tokens > (1 << 20) || !x || !counts || !routes || !y || (input_mode != 0 && input_mode != 1) ||
+        (y_dtype != DIH_F32 && y_dtype != DIH_BF16)) {
+        set_error(error, capacity, "Invalid grouped qmm arguments");
+        return -1;
+    }
+    if (up && (up->experts != m->experts || up->rows != m->rows || up->columns != m->columns || up->bits != m->bits)) {
+        set_error(error, capacity, "Gate and up matrices must share shape and bits");
+        return -1;
+    }
+    if (!sync_matrix(m, error, capacity) || (up && !sync_matrix(up, error, capacity))) return -1;
+    hipStream_t s = pick(c, stream);
+    ProfScope prof_scope(c);
+    QmmArgs a;
+    a.m0 = m; a.m1 = up; a.tokens = tokens; a.routes = routes; a.counts = counts; a.ngroups = m->experts;
+    a.x = static_cast<const uint16_t *>(x); a.in_mode = input_mode; a.y = y; a.y_bf16 = y_dtype == DIH_BF16;
+    const bool ok = launch_qmm(a, s, error, capacity);
+    prof_mark(c, s, up ? "grouped_gate_up" : "grouped_qmm");
+    return ok ? 0 : -1;
+}
+
 __attribute__((visibility("default"))) int dih_dense(void *ctx, void *matrix, int tokens, const void *x, void *y,
                                                      int y_dtype, void *stream, char *error, int capacity) {
     Context *c = as_ctx(ctx);

@@ -83,7 +83,7 @@ EXPORTS = [
     "dih_quant_batch", "dih_quant_matvec", "dih_quant_experts", "dih_quant_embedding",
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
     "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm",
-    "dih_moe_prefill_norm", "dih_dense", "dih_attention",
+    "dih_moe_prefill_norm", "dih_grouped_qmm", "dih_dense", "dih_attention",
     "dih_attention_partition", "dih_delta_rule", "dih_delta_create", "dih_delta_destroy",
     "dih_delta_step", "dih_set_profiling",
     "dih_profile_read", "dih_version",
@@ -137,6 +137,7 @@ def load():
         "dih_moe_decode_norm": ([P, P, P, P, P, P, P, P, E, I], I),
         "dih_moe_prefill_norm": ([P, P, I, P, P, I, P, P, P, P, E, I], I),
         "dih_dense": ([P, P, I, P, P, I, P, E, I], I),
+        "dih_grouped_qmm": ([P, P, P, I, P, I, P, P, P, I, P, E, I], I),
         "dih_attention": ([P, P, I, P, P, I, P, I, P, I, I, I, I, P, E, I], I),
         "dih_attention_partition": ([I, I, I], I),
         "dih_delta_rule": ([P, P, P, P, P, P, P, P, I, I, P, E, I], I),
@@ -588,6 +589,16 @@ def moe_prefill(dev, layer: MoeLayer, tokens, x, logits, residual, logits_dtype=
                                          logits_dtype, _dp(residual), None if merge is None else ctypes.byref(merge),
                                          None if trace is None else ctypes.byref(trace), _stream(stream), err,
                                          _ERR), err, ArgumentError)
+
+
+def grouped_qmm(dev, m, tokens, x, counts, routes, y, up=None, input_mode=0, y_dtype=F32, stream=None) -> None:
+    """One grouped expert projection over dih_build_groups route lists (dih_grouped_qmm):
+    gate/up + SwiGLU when `up` is given (input_mode 1: token rows), else a plain grouped
+    product (input_mode 0: route rows)."""
+    err = _errbuf()
+    _check(dev._lib.dih_grouped_qmm(_ctx(dev), m.handle, None if up is None else up.handle, tokens, _dp(x),
+                                    input_mode, _dp(counts), _dp(routes), _dp(y), y_dtype, _stream(stream), err,
+                                    _ERR), err, ArgumentError)
 
 
 def dense(dev, m, tokens, x, y, y_dtype=F32, stream=None) -> None:

@@ -252,20 +252,6 @@ typedef struct orc_moe_layer {
     const orc_matrix *shared_gate, *shared_up, *shared_down, *shared_route;
 } orc_moe_layer;
 
-/* One token's SwiGLU activation for expert e of (gate, up) over input xd (double). */
-static void swiglu_row(const orc_matrix *g, const orc_matrix *u, int e, const double *xd,
-                       int round_w, double *act) {
-    int I = g->rows, C = g->columns;
-    for (int i = 0; i < I; i++) {
-        double a = 0, b = 0;
-        for (int c = 0; c < C; c++) {
-            a += weight_at(g, e, i, c, round_w) * xd[c];
-            b += weight_at(u, e, i, c, round_w) * xd[c];
-        }
-        act[i] = a * sigmoid_d(a) * b;
-    }
-}
-
 /* MoE block in fp64 for T tokens given the selected ids/probs per token
  * (Moe Qwen36Model.cs:218-245; merge order of prefill_merge gpu_prefill.mm:140-150:
  * y = shared*sigmoid(route) then += expert_slot*p_slot for slot 0..7).
@@ -274,56 +260,99 @@ static void swiglu_row(const orc_matrix *g, const orc_matrix *u, int e, const do
  * (prefill_expert_packed.mm:34; expanded_pack prefill_bf16_expanded.mm:24).
  * y_out f64 [T][H] receives the MoE output before it is added to the residual;
  * route_out (optional) f64 [T*8 + T][H] receives per-route down outputs. */
+/* Dequantized weights of expert e of m in double, row-major [rows][columns]. */
+static void dequant_expert(const orc_matrix *m, int e, int round_w, double *out) {
+    for (int r = 0; r < m->rows; r++)
+        for (int c = 0; c < m->columns; c++) out[(size_t)r * m->columns + c] = weight_at(m, e, r, c, round_w);
+}
+
 ORC_API void orc_moe_f64(const orc_moe_layer *L, int tokens, const float *x,
                          const int32_t *ids, const float *probs, int bf16_operands,
                          double *y_out, double *route_out) {
-    int H = L->gate->columns, I = L->gate->rows, Is = L->shared_gate->rows;
+    int H = L->gate->columns, I = L->gate->rows, Is = L->shared_gate->rows, E = L->gate->experts;
     int Imax = I > Is ? I : Is;
+    size_t T = (size_t)tokens;
+    /* Work is grouped by expert: each expert's weights are dequantized once and applied to
+     * all of its routes; every dot product keeps its summation order (columns ascending
+     * for gate/up, intermediate index ascending for down), so each route's output and the
+     * merged sum below are the same numbers as a token-by-token evaluation. */
+    double *ro = route_out ? route_out : (double *)malloc(sizeof(double) * T * 9 * (size_t)H);
+    double *xd = (double *)malloc(sizeof(double) * T * (size_t)H);
+    int *order = (int *)malloc(sizeof(int) * T * 8);
+    int *start = (int *)calloc((size_t)E + 1, sizeof(int));
+    for (size_t i = 0; i < T * (size_t)H; i++) xd[i] = bf16_operands ? (double)round_bf(x[i]) : (double)x[i];
+    for (size_t r = 0; r < T * 8; r++) start[ids[r] + 1]++;
+    for (int e = 0; e < E; e++) start[e + 1] += start[e];
+    {
+        int *fill = (int *)malloc(sizeof(int) * (size_t)E);
+        memcpy(fill, start, sizeof(int) * (size_t)E);
+        for (size_t r = 0; r < T * 8; r++) order[fill[ids[r]]++] = (int)r;   /* routes ascending */
+        free(fill);
+    }
 #pragma omp parallel
     {
-        double *xd = (double *)malloc(sizeof(double) * (size_t)H);
+        double *wg = (double *)malloc(sizeof(double) * (size_t)Imax * H);
+        double *wu = (double *)malloc(sizeof(double) * (size_t)Imax * H);
+        double *wd = (double *)malloc(sizeof(double) * (size_t)H * Imax);
         double *act = (double *)malloc(sizeof(double) * (size_t)Imax);
-        double *o = (double *)malloc(sizeof(double) * (size_t)H);
+        /* group -1 is the shared expert (every token), then the routed experts */
 #pragma omp for schedule(dynamic)
-        for (int t = 0; t < tokens; t++) {
-            for (int c = 0; c < H; c++) {
-                float v = x[(size_t)t * H + c];
-                xd[c] = bf16_operands ? (double)round_bf(v) : (double)v;
-            }
-            double *y = y_out + (size_t)t * H;
-            /* shared expert and its sigmoid gate (shared_route is never rounded: the
-             * reference evaluates it with the fp32 GEMV, gpu_prefill.mm:700). */
-            swiglu_row(L->shared_gate, L->shared_up, 0, xd, bf16_operands, act);
-            if (bf16_operands)
-                for (int i = 0; i < Is; i++) act[i] = (double)round_bf((float)act[i]);
-            double route = 0;
-            for (int c = 0; c < H; c++) route += weight_at(L->shared_route, 0, 0, c, 0) * (double)x[(size_t)t * H + c];
-            double gate = sigmoid_d(route);
-            for (int h = 0; h < H; h++) {
-                double acc = 0;
-                for (int i = 0; i < Is; i++) acc += weight_at(L->shared_down, 0, h, i, bf16_operands) * act[i];
-                o[h] = acc;
-                if (route_out) route_out[((size_t)tokens * 8 + t) * H + h] = acc;
-                y[h] = acc * gate;
-            }
-            for (int s = 0; s < 8; s++) {
-                int e = ids[t * 8 + s];
-                swiglu_row(L->gate, L->up, e, xd, bf16_operands, act);
-                if (bf16_operands)
-                    for (int i = 0; i < I; i++) act[i] = (double)round_bf((float)act[i]);
-                double p = (double)probs[t * 8 + s];
+        for (int g = -1; g < E; g++) {
+            const int shared = g < 0, n = shared ? tokens : start[g + 1] - start[g];
+            if (n == 0) continue;
+            const orc_matrix *mg = shared ? L->shared_gate : L->gate, *mu = shared ? L->shared_up : L->up;
+            const orc_matrix *md = shared ? L->shared_down : L->down;
+            const int e = shared ? 0 : g, In = mg->rows;
+            dequant_expert(mg, e, bf16_operands, wg);
+            dequant_expert(mu, e, bf16_operands, wu);
+            dequant_expert(md, e, bf16_operands, wd);
+            for (int k = 0; k < n; k++) {
+                const size_t route = shared ? T * 8 + (size_t)k : (size_t)order[start[g] + k];
+                const double *xt = xd + (shared ? (size_t)k : route / 8) * H;
+                for (int i = 0; i < In; i++) {
+                    double a = 0, b = 0;
+                    const double *gi = wg + (size_t)i * H, *ui = wu + (size_t)i * H;
+                    for (int c = 0; c < H; c++) {
+                        a += gi[c] * xt[c];
+                        b += ui[c] * xt[c];
+                    }
+                    act[i] = a * sigmoid_d(a) * b;
+                    if (bf16_operands) act[i] = (double)round_bf((float)act[i]);
+                }
                 for (int h = 0; h < H; h++) {
                     double acc = 0;
-                    for (int i = 0; i < I; i++) acc += weight_at(L->down, e, h, i, bf16_operands) * act[i];
-                    if (route_out) route_out[((size_t)t * 8 + s) * H + h] = acc;
-                    y[h] += acc * p;
+                    const double *dh = wd + (size_t)h * In;
+                    for (int i = 0; i < In; i++) acc += dh[i] * act[i];
+                    ro[route * H + h] = acc;
                 }
             }
         }
-        free(xd);
+        free(wg);
+        free(wu);
+        free(wd);
         free(act);
-        free(o);
+        /* merge in the reference's order: shared * sigmoid(route), then slots 0..7. The
+         * shared expert's sigmoid gate is never rounded: the reference evaluates it with
+         * the fp32 GEMV (gpu_prefill.mm:700). */
+#pragma omp for schedule(static)
+        for (int t = 0; t < tokens; t++) {
+            double route = 0;
+            for (int c = 0; c < H; c++) route += weight_at(L->shared_route, 0, 0, c, 0) * (double)x[(size_t)t * H + c];
+            const double gate = sigmoid_d(route);
+            double *y = y_out + (size_t)t * H;
+            const double *so = ro + (T * 8 + (size_t)t) * H;
+            for (int h = 0; h < H; h++) y[h] = so[h] * gate;
+            for (int s = 0; s < 8; s++) {
+                const double p = (double)probs[t * 8 + s];
+                const double *o = ro + ((size_t)t * 8 + s) * H;
+                for (int h = 0; h < H; h++) y[h] += o[h] * p;
+            }
+        }
     }
+    if (!route_out) free(ro);
+    free(xd);
+    free(order);
+    free(start);
 }
 
 /* ---------------- reference-faithful fp32 CPU path (the CPU baseline) -------------- */

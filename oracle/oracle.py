@@ -188,6 +188,20 @@ def dense_f64(m: QMatrix, x: np.ndarray, expert=0, round_operands=True) -> np.nd
     return y
 
 
+def dense_f64_blas(m: QMatrix, x: np.ndarray, expert=0, round_operands=True) -> np.ndarray:
+    """The product of dense_f64 (Y[t][r] = sum_c w(e,r,c) X[t][c], prefill_bf16_product
+    prefill_bf16.mm:26-37) for chunk sizes where a scalar loop is too slow: weights from the
+    numpy dequantization, operands widened to float64 and multiplied by BLAS. With
+    round_operands the bf16 products are exact in float64, so the result differs from
+    dense_f64 only in the order of the float64 sums."""
+    x = np.asarray(x, dtype=np.float32)
+    one = QMatrix(m.packed.reshape(m.experts, -1)[expert], m.scales.reshape(m.experts, -1)[expert],
+                  m.biases.reshape(m.experts, -1)[expert], 1, m.rows, m.columns, m.bits)
+    w = one.dequant(round_bf=round_operands)[0].astype(np.float64)
+    xd = (round_bf16(x) if round_operands else x).astype(np.float64)
+    return xd @ w.T
+
+
 def top8(logits: np.ndarray):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     ids = np.zeros(8, dtype=np.int32)

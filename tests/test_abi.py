@@ -55,3 +55,19 @@ def test_host_side_argument_validation_without_gpu():
     """Validation that happens before any device call (QuantizedMetal.cs:14, 34-36)."""
     with pytest.raises(dh.ArgumentOutOfRangeError):
         dh.QuantizedHip(residency_refresh_milliseconds=60001)
+
+
+# Every entry point the reference's P/Invoke table binds (QuantNative,
+# QuantizedMetal.cs:242-274); each needs a dih_ counterpart for the drop-in swap.
+REFERENCE_QUANT_NATIVE = [
+    "di_quant_create", "di_quant_create_configured", "di_quant_destroy", "di_quant_residency_bytes",
+    "di_quant_residency_prepare", "di_quant_matrix_create", "di_quant_matrix_buffer", "di_quant_matrix_destroy",
+    "di_quant_batch", "di_quant_matvec", "di_quant_experts", "di_quant_embedding",
+    "di_delta_create", "di_delta_destroy", "di_delta_step",
+]
+
+
+def test_every_reference_native_entry_has_a_counterpart():
+    names = set(declared())
+    missing = [n for n in REFERENCE_QUANT_NATIVE if "dih_" + n[3:] not in names]
+    assert not missing, missing

@@ -143,3 +143,57 @@ def test_delta_rule_arguments_are_validated(device):
         dh.delta_rule(device, s, None, c, ab, ab, c, out, 4)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all()) and bool((s == 1.0).all()) and bool((h == 1.0).all())
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_delta_memory_steps_match_recurrence(device, mode):
+    """DeltaMemory (di_delta_create / di_delta_step, quantized.mm:398-423): a zeroed state
+    stepped one token at a time from host arrays equals the recurrence from a zero state,
+    at the same bar as the chunk path."""
+    conv, a, b, _, _, _ = _oracle(mode)
+    T = 40
+    want_out, want_state = orc.delta_rule_f64(np.zeros((32, 128, 128)), conv, a, b, T)
+    mem = device.new_delta_memory()
+    try:
+        got = np.zeros((T, 4096), dtype=np.float32)
+        for t in range(T):
+            out = np.full(4096, np.nan, dtype=np.float32)
+            mem.step(conv[t, :2048], conv[t, 2048:4096], conv[t, 4096:], a[t], b[t], out)
+            got[t] = out
+        diff = np.abs(got - want_out)
+        assert np.all(np.isfinite(got)) and np.max(diff) <= 1e-5, np.max(diff)
+        rel = np.sqrt(np.sum(diff ** 2) / max(np.sum(want_out ** 2), 1e-30))
+        assert rel <= 3e-5, rel
+    finally:
+        mem.dispose()
+
+
+def test_delta_memory_validation(device):
+    """DeltaMemory.Step's dimension check (QuantizedMetal.cs:216-217) and the native null
+    check (quantized.mm:410) reject before any GPU work; a second memory is independent."""
+    mem = device.new_delta_memory()
+    other = device.new_delta_memory()
+    try:
+        z = np.zeros
+        with pytest.raises(dh.ArgumentError, match="Unsupported gated-delta dimensions"):
+            mem.step(z(2048), z(2048), z(4095), z(32), z(32), z(4096))
+        err = dh._errbuf()
+        ms = __import__("ctypes").c_double()
+        arr = np.zeros(4096, dtype=np.float32)
+        rc = device._lib.dih_delta_step(device.context, mem.handle, None, arr.ctypes.data, arr.ctypes.data,
+                                        arr.ctypes.data, arr.ctypes.data, arr.ctypes.data, None, err, dh._ERR)
+        assert rc == -1 and dh._msg(err) == "Null delta argument"
+        # one step on `mem` with decay 1, beta 1, a unit key and value 1 leaves S = v k^T there
+        k = np.zeros(2048, dtype=np.float32)
+        k[0] = 1.0
+        q = k.copy()
+        v = np.ones(4096, dtype=np.float32)
+        out = np.zeros(4096, dtype=np.float32)
+        mem.step(q, k, v, np.ones(32), np.ones(32), out)
+        assert np.allclose(out[:128], 1.0) and np.allclose(out[2 * 128:3 * 128], 0.0)   # head 2 -> key head 1
+        out2 = np.zeros(4096, dtype=np.float32)
+        other.step(q, k, np.zeros(4096), np.ones(32), np.ones(32), out2)
+        assert np.all(out2 == 0.0)
+    finally:
+        mem.dispose()
+        other.dispose()

@@ -507,3 +507,73 @@ def test_delta_history_roll():
     assert np.array_equal(orc.delta_history(hist, raw, 1), np.stack([hist[1], hist[2], raw[0]]))
     assert np.array_equal(orc.delta_history(hist, raw, 2), np.stack([hist[2], raw[0], raw[1]]))
     assert np.array_equal(orc.delta_history(hist, raw, 5), raw[2:5])
+
+
+@pytest.mark.parametrize("rounded", [False, True])
+def test_moe_f64_sigmoid_gated_combine_closed_form(rounded):
+    """The sigma-gated combine (Moe, Qwen36Model.cs:230-244) by a closed form. With every
+    code 0 and scale 1, each weight equals its row's bias, so a row of any matrix reduces to
+    b_row * sum(x): gate_i = bg_i S, up_i = bu_i S with S = sum(x), act_i = silu(gate_i) up_i,
+    down_h = bd_h sum_i act_i, and the shared route is sigmoid(br S). Hence
+        y[h] = sigmoid(br S) bsd_h A_shared + sum_slot p_slot bd[e_slot]_h A[e_slot]
+    with A = sum_i act_i. One-hot probabilities leave the shared term plus one expert."""
+    E, H, I = 12, 128, 64
+
+    def const_rows(experts, rows, cols, vals):
+        bias = np.repeat(orc.f32_to_bf16_bits(vals.astype(np.float32)).reshape(experts, rows, 1), cols // 64, axis=2)
+        return orc.QMatrix(np.zeros(experts * rows * cols * 8 // 32, np.uint32),
+                           np.full(experts * rows * (cols // 64), 0x3F80, np.uint16), bias, experts, rows, cols, 8)
+
+    e_, r_ = np.meshgrid(np.arange(E), np.arange(I), indexing="ij")
+    bg = ((e_ * 3 + r_) % 7 - 3) / 32.0
+    bu = ((e_ + r_ * 5) % 5 + 1) / 64.0
+    e2, h2 = np.meshgrid(np.arange(E), np.arange(H), indexing="ij")
+    bd = ((e2 * 5 + h2 * 3) % 9 - 4) / 16.0
+    bsg = (np.arange(I) % 3 - 1) / 8.0
+    bsu = (np.arange(I) % 4 + 1) / 16.0
+    bsd = (np.arange(H) % 5 - 2) / 4.0
+    br = np.array([0.375])
+    L = orc.MoeLayer(None, const_rows(E, I, H, bg), const_rows(E, I, H, bu), const_rows(E, H, I, bd),
+                     const_rows(1, I, H, bsg), const_rows(1, I, H, bsu), const_rows(1, H, I, bsd),
+                     const_rows(1, 1, H, br))
+    T = 3
+    x = np.zeros((T, H), dtype=np.float32)
+    x[0, :4] = [0.5, 0.25, -0.125, 1.0]           # S = 1.625
+    x[1, 10] = -2.0                                # S = -2
+    x[2, ::2] = 0.015625                           # S = 1
+    ids = np.array([[3, 0, 7, 11, 1, 2, 4, 5], [6, 8, 9, 10, 0, 1, 2, 3], [2, 4, 6, 8, 10, 11, 1, 0]], np.int32)
+    probs = np.zeros((T, 8), dtype=np.float32)
+    probs[0] = [0.5, 0.25, 0.125, 0.0625, 0.03125, 0.015625, 0.0078125, 0.0078125]
+    probs[1, 0] = 1.0                              # one-hot: the shared term plus expert 6
+    probs[2] = 0.125
+    y = orc.moe_f64(L, x, ids, probs, bf16_operands=rounded)
+
+    def silu(v):
+        return v / (1 + np.exp(-v))
+
+    def act_sum(g_rows, u_rows, S):
+        a = silu(g_rows * S) * (u_rows * S)
+        if rounded:
+            a = orc.round_bf16(a.astype(np.float32)).astype(np.float64)
+        return a.sum()
+
+    for t in range(T):
+        S = float(x[t].astype(np.float64).sum())
+        want = 1 / (1 + np.exp(-br[0] * S)) * bsd * act_sum(bsg, bsu, S)
+        for s in range(8):
+            e = ids[t, s]
+            want = want + float(probs[t, s]) * bd[e] * act_sum(bg[e], bu[e], S)
+        assert np.max(np.abs(y[t] - want)) <= 1e-12 * max(1.0, np.abs(want).max()), t
+
+
+def test_dense_blas_matches_dense_f64():
+    """dense_f64_blas (the BLAS form used at full chunk sizes) against the scalar dense_f64,
+    both rounding modes, an expert other than 0 and both bit widths."""
+    rng = np.random.default_rng(41)
+    for bits in (5, 8):
+        m = orc.random_matrix(rng, 3, 70, 384, bits)
+        x = rng.normal(size=(9, 384)).astype(np.float32)
+        for rnd in (False, True):
+            a = orc.dense_f64(m, x, expert=2, round_operands=rnd)
+            b = orc.dense_f64_blas(m, x, expert=2, round_operands=rnd)
+            assert np.max(np.abs(a - b)) <= 1e-12 * np.abs(a).max()

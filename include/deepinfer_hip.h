@@ -216,6 +216,21 @@ int dih_moe_decode_norm(void *context, const dih_moe_layer *layer, const void *x
                         const float *logits, void *residual, const dih_moe_merge *merge,
                         const dih_moe_trace *trace, void *stream, char *error, int capacity);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * dih_moe_decode_norm with the same arguments, kernels and results, whose intermediate
+ * buffers come from a fixed 128 KiB device array that the library holds on every GPU it
+ * runs on until the process ends, instead of the context's grow-only scratch. It calls no
+ * hipMalloc or hipFree and records no profiling events. Limit: the step's buffers
+ * (256-byte aligned: logits [E], SwiGLU rows [8*I + Is], shared down [H], ids, probs and
+ * 128 router candidates) must fit in 128 KiB; every layer shape the MoE entry points accept
+ * (E <= 256, I and Is <= 2048, H <= 8192) does, and a larger one is rejected with an error.
+ * Calls on one GPU share that array (it keeps the last call's contents; nothing in it needs
+ * clearing): calls that overlap on one GPU, from any context or stream, race. */
+int dih_moe_decode_noalloc(void *context, const dih_moe_layer *layer, const void *x,
+                           const float *logits, void *residual, const dih_moe_merge *merge,
+                           const dih_moe_trace *trace, void *stream, char *error, int capacity);
+
 /* Prefill MoE chunk (gpu_prefill.mm:700-706 with packed_expert_gate_fused /
  * packed_expert_down, prefill_expert_packed.mm, and prefill_merge gpu_prefill.mm:140-150):
  * top-8 of logits (bf16 or f32 [T][E]) -> grouped per-expert route lists -> bf16 MFMA

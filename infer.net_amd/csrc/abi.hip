@@ -4,10 +4,45 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <new>
 #include <string>
 
 #include "dih_internal.h"
+
+// Fixed device scratch of dih_moe_decode_noalloc, the entry point for callers that cannot
+// allocate. Every GPU holds its own copy at its own address for the life of the process.
+// Host code never uses this name as a device pointer: the address of this device's copy
+// comes from hipGetSymbolAddress (noalloc_scratch_address below) and is kept per device.
+static constexpr size_t kNoAllocScratchBytes = 128 * 1024;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mutex;
+bool g_noalloc_done[kMaxDevices];
+void *g_noalloc_ptr[kMaxDevices];
+hipError_t g_noalloc_rc[kMaxDevices];
+
+// Device address of `scratch` on device `dev`, which must be the current device; looked up
+// once per device.
+void *noalloc_scratch_address(int dev, std::string &why) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        why = "device index out of range for the no-allocation scratch";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (!g_noalloc_done[dev]) {
+        void *ptr = nullptr;
+        g_noalloc_rc[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_noalloc_ptr[dev] = g_noalloc_rc[dev] == hipSuccess ? ptr : nullptr;
+        g_noalloc_done[dev] = true;
+    }
+    if (!g_noalloc_ptr[dev])
+        why = std::string("no-allocation scratch lookup failed: ") + hipGetErrorString(g_noalloc_rc[dev]);
+    return g_noalloc_ptr[dev];
+}
+}  // namespace
 
 namespace dih {
 
@@ -25,7 +60,7 @@ bool hip_ok(hipError_t e, char *error, int capacity, const char *what) {
     return false;
 }
 
-void *scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity) {
+void *ctx_scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity) {
     Scratch &s = c->ws[id];
     if (bytes == 0) bytes = 4;
     if (s.bytes >= bytes) return s.ptr;
@@ -177,6 +212,8 @@ __attribute__((visibility("default"))) void *dih_quant_create_configured(int res
     }
     c->device = dev;
     c->resident = resident == 1;
+    // a failed lookup only disables dih_moe_decode_noalloc (which then reports it)
+    c->noalloc = noalloc_scratch_address(dev, c->noalloc_error);
     if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamDefault), error, capacity, "stream") ||
         !hip_ok(hipEventCreate(&c->start), error, capacity, "event") ||
         !hip_ok(hipEventCreate(&c->stop), error, capacity, "event")) {
@@ -356,7 +393,7 @@ __attribute__((visibility("default"))) int dih_quant_batch(void *ctx, const dih_
                 return -1;
             }
     }
-    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
+    uint32_t *ids = static_cast<uint32_t *>(ctx_scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
     if (!ids) return -1;
     hipStream_t s = c->stream;
     for (int j = 0; j < count; j++) {
@@ -441,8 +478,8 @@ __attribute__((visibility("default"))) int dih_quant_experts(void *ctx, void *ga
         }
     hipStream_t s = c->stream;
     const int I = gate->rows, H = down->rows;
-    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
-    float *act = static_cast<float *>(scratch(c, S_ACT, (size_t)8 * I * 4, error, capacity));
+    uint32_t *ids = static_cast<uint32_t *>(ctx_scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
+    float *act = static_cast<float *>(ctx_scratch(c, S_ACT, (size_t)8 * I * 4, error, capacity));
     if (!ids || !act) return -1;
     if (!sync_matrix(gate, error, capacity) || !sync_matrix(up, error, capacity) ||
         !sync_matrix(down, error, capacity) || !sync_matrix(shared, error, capacity) ||
@@ -492,7 +529,7 @@ __attribute__((visibility("default"))) int dih_quant_embedding(void *matrix, int
     if (!m || !out || token < 0 || token >= m->rows || m->experts != 1) return -1;
     char err[256];
     Context *c = m->ctx;
-    float *dev = static_cast<float *>(scratch(c, S_STAGE_Y, (size_t)m->columns * 4, err, sizeof(err)));
+    float *dev = static_cast<float *>(ctx_scratch(c, S_STAGE_Y, (size_t)m->columns * 4, err, sizeof(err)));
     if (!dev || !sync_matrix(m, err, sizeof(err))) return -1;
     if (!launch_embedding(m, token, dev, c->stream, err, sizeof(err))) return -1;
     if (hipStreamSynchronize(c->stream) != hipSuccess) return -1;
@@ -553,8 +590,8 @@ __attribute__((visibility("default"))) int dih_argmax(void *ctx, const float *va
         return -1;
     }
     const size_t parts = (size_t)(n + kArgmaxPer - 1) / kArgmaxPer;
-    float *pv = static_cast<float *>(scratch(c, S_ARGVAL, parts * 4, error, capacity));
-    uint32_t *pi = static_cast<uint32_t *>(scratch(c, S_ARGIDX, parts * 4, error, capacity));
+    float *pv = static_cast<float *>(ctx_scratch(c, S_ARGVAL, parts * 4, error, capacity));
+    uint32_t *pi = static_cast<uint32_t *>(ctx_scratch(c, S_ARGIDX, parts * 4, error, capacity));
     if (!pv || !pi) return -1;
     hipStream_t s = pick(c, stream);
     return launch_argmax(values, n, pv, pi, next, s, error, capacity) ? 0 : -1;
@@ -585,8 +622,8 @@ __attribute__((visibility("default"))) int dih_lm_head(void *ctx, void *const *s
     for (int i = 0; i < slice_count; i++)
         if (!sync_matrix(as_mat(slices[i]), error, capacity)) return -1;
     const size_t parts = (size_t)(total + kArgmaxPer - 1) / kArgmaxPer;
-    float *pv = static_cast<float *>(scratch(c, S_ARGVAL, parts * 4, error, capacity));
-    uint32_t *pi = static_cast<uint32_t *>(scratch(c, S_ARGIDX, parts * 4, error, capacity));
+    float *pv = static_cast<float *>(ctx_scratch(c, S_ARGVAL, parts * 4, error, capacity));
+    uint32_t *pi = static_cast<uint32_t *>(ctx_scratch(c, S_ARGIDX, parts * 4, error, capacity));
     if (!pv || !pi) return -1;
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);
@@ -706,15 +743,45 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
     return dih_moe_decode_norm(ctx, L, x, logits, residual, nullptr, trace, stream, error, capacity);
 }
 
-__attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const dih_moe_layer *L, const void *x,
-                                                               const float *logits, void *residual,
-                                                               const dih_moe_merge *merge,
-                                                               const dih_moe_trace *trace, void *stream,
-                                                               char *error, int capacity) {
-    Context *c = as_ctx(ctx);
+namespace dih {
+// Device buffers of one decode MoE step (all fully written before they are read, so none
+// needs clearing): logits [E], shared route [1], shared SwiGLU [Is], slot SwiGLU [8*I],
+// shared down [H], ids [8], probs [8], status [1], router candidates [128] float2.
+struct DecodeBuffers {
+    float *lg, *srt, *sact, *act, *sout, *probs;
+    uint32_t *ids, *status;
+    float2 *cand;
+};
+
+// Carves the step's buffers from `base` at 256-byte boundaries; returns the bytes used.
+static size_t carve_decode(unsigned char *base, int E, int H, int I, int Is, DecodeBuffers &b) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        unsigned char *p = base ? base + off : nullptr;
+        off += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    b.lg = reinterpret_cast<float *>(take((size_t)E * 4));
+    b.srt = reinterpret_cast<float *>(take(16));
+    b.sact = reinterpret_cast<float *>(take((size_t)Is * 4));
+    b.act = reinterpret_cast<float *>(take((size_t)8 * I * 4));
+    b.sout = reinterpret_cast<float *>(take((size_t)H * 4));
+    b.ids = reinterpret_cast<uint32_t *>(take(8 * 8 * 4));
+    b.probs = reinterpret_cast<float *>(take(8 * 4));
+    b.status = reinterpret_cast<uint32_t *>(take(16));
+    b.cand = reinterpret_cast<float2 *>(take(128 * sizeof(float2)));
+    return off;
+}
+
+// The decode MoE step. `fixed` null: buffers from the context's grow-only scratch (which
+// may allocate) and per-stage profiling; otherwise buffers carved from `fixed` (at most
+// `fixed_bytes`) with no allocation and no profiling events.
+static int moe_decode(Context *c, const dih_moe_layer *L, const void *x, const float *logits, void *residual,
+                      const dih_moe_merge *merge, const dih_moe_trace *trace, void *stream,
+                      unsigned char *fixed, size_t fixed_bytes, char *error, int capacity) {
     int E, H, I, Is;
     MergeOut mo;
-    if (!c || !x || !residual) {
+    if (!x || !residual) {
         set_error(error, capacity, "Invalid decode MoE arguments");
         return -1;
     }
@@ -727,20 +794,37 @@ __attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const 
     Matrix *gate = as_mat(L->gate), *up = as_mat(L->up), *down = as_mat(L->down);
     Matrix *sg = as_mat(L->shared_gate), *su = as_mat(L->shared_up), *sd = as_mat(L->shared_down);
     Matrix *sr = as_mat(L->shared_route), *router = as_mat(L->router);
-    float *lg = static_cast<float *>(scratch(c, S_LOGITS, (size_t)E * 4, error, capacity));
-    float *srt = static_cast<float *>(scratch(c, S_SROUTE, 16, error, capacity));
-    float *sact = static_cast<float *>(scratch(c, S_SACT, (size_t)Is * 4, error, capacity));
-    float *act = static_cast<float *>(scratch(c, S_ACT, (size_t)8 * I * 4, error, capacity));
-    float *sout = static_cast<float *>(scratch(c, S_SOUT, (size_t)H * 4, error, capacity));
-    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
-    float *probs = static_cast<float *>(scratch(c, S_PROBS, 8 * 4, error, capacity));
-    uint32_t *status = static_cast<uint32_t *>(scratch(c, S_STATUS, 16, error, capacity));
-    if (!lg || !srt || !sact || !act || !sout || !ids || !probs || !status) return -1;
+    DecodeBuffers bufs;
+    if (fixed) {
+        const size_t need = carve_decode(nullptr, E, H, I, Is, bufs);
+        if (need > fixed_bytes) {
+            set_error(error, capacity, "Decode MoE step needs " + std::to_string(need) +
+                                           " bytes of scratch; the no-allocation scratch holds " +
+                                           std::to_string(fixed_bytes));
+            return -1;
+        }
+        carve_decode(fixed, E, H, I, Is, bufs);
+    } else {
+        bufs.lg = static_cast<float *>(ctx_scratch(c, S_LOGITS, (size_t)E * 4, error, capacity));
+        bufs.srt = static_cast<float *>(ctx_scratch(c, S_SROUTE, 16, error, capacity));
+        bufs.sact = static_cast<float *>(ctx_scratch(c, S_SACT, (size_t)Is * 4, error, capacity));
+        bufs.act = static_cast<float *>(ctx_scratch(c, S_ACT, (size_t)8 * I * 4, error, capacity));
+        bufs.sout = static_cast<float *>(ctx_scratch(c, S_SOUT, (size_t)H * 4, error, capacity));
+        bufs.ids = static_cast<uint32_t *>(ctx_scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
+        bufs.probs = static_cast<float *>(ctx_scratch(c, S_PROBS, 8 * 4, error, capacity));
+        bufs.status = static_cast<uint32_t *>(ctx_scratch(c, S_STATUS, 16, error, capacity));
+        bufs.cand = static_cast<float2 *>(ctx_scratch(c, S_CAND, 128 * sizeof(float2), error, capacity));
+        if (!bufs.lg || !bufs.srt || !bufs.sact || !bufs.act || !bufs.sout || !bufs.ids || !bufs.probs ||
+            !bufs.status || !bufs.cand)
+            return -1;
+    }
+    float *lg = bufs.lg, *srt = bufs.srt, *sact = bufs.sact, *act = bufs.act, *sout = bufs.sout;
+    uint32_t *ids = bufs.ids;
+    float *probs = bufs.probs;
     hipStream_t s = pick(c, stream);
-    ProfScope prof_scope(c);
+    ProfScope prof_scope(fixed ? nullptr : c);
     if (decode_fast_path_ok(router, gate, down, sg, sd, sr)) {
-        float2 *cand = static_cast<float2 *>(scratch(c, S_CAND, 128 * sizeof(float2), error, capacity));
-        if (!cand) return -1;
+        float2 *cand = bufs.cand;
         DecodeLaunch a;
         a.router = router; a.gate = gate; a.up = up; a.down = down;
         a.shared_gate = sg; a.shared_up = su; a.shared_down = sd; a.shared_route = sr;
@@ -827,6 +911,38 @@ __attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const 
     }
     return 0;
 }
+}  // namespace dih
+
+__attribute__((visibility("default"))) int dih_moe_decode_norm(void *ctx, const dih_moe_layer *L, const void *x,
+                                                               const float *logits, void *residual,
+                                                               const dih_moe_merge *merge,
+                                                               const dih_moe_trace *trace, void *stream,
+                                                               char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c) {
+        set_error(error, capacity, "Invalid decode MoE arguments");
+        return -1;
+    }
+    return moe_decode(c, L, x, logits, residual, merge, trace, stream, nullptr, 0, error, capacity);
+}
+
+__attribute__((visibility("default"))) int dih_moe_decode_noalloc(void *ctx, const dih_moe_layer *L, const void *x,
+                                                                  const float *logits, void *residual,
+                                                                  const dih_moe_merge *merge,
+                                                                  const dih_moe_trace *trace, void *stream,
+                                                                  char *error, int capacity) {
+    Context *c = as_ctx(ctx);
+    if (!c) {
+        set_error(error, capacity, "Invalid decode MoE arguments");
+        return -1;
+    }
+    if (!c->noalloc) {
+        set_error(error, capacity, c->noalloc_error);
+        return -1;
+    }
+    return moe_decode(c, L, x, logits, residual, merge, trace, stream, static_cast<unsigned char *>(c->noalloc),
+                      kNoAllocScratchBytes, error, capacity);
+}
 
 __attribute__((visibility("default"))) int dih_moe_prefill(void *ctx, const dih_moe_layer *L, int tokens,
                                                            const void *x, const void *logits, int logits_dtype,
@@ -860,12 +976,12 @@ __attribute__((visibility("default"))) int dih_moe_prefill_norm(void *ctx, const
         return -1;
     }
     const size_t T = (size_t)tokens, routes_n = T * 9;
-    uint32_t *ids = static_cast<uint32_t *>(scratch(c, S_IDS, std::max<size_t>(T * 8 * 4, 256), error, capacity));
-    float *probs = static_cast<float *>(scratch(c, S_PROBS, T * 8 * 4, error, capacity));
-    uint32_t *counts = static_cast<uint32_t *>(scratch(c, S_COUNTS, (size_t)(E + 1) * 4, error, capacity));
-    uint32_t *routes = static_cast<uint32_t *>(scratch(c, S_ROUTES, (size_t)(E + 1) * T * 4, error, capacity));
-    uint16_t *actb = static_cast<uint16_t *>(scratch(c, S_ACTBF, routes_n * I * 2, error, capacity));
-    float *rout = static_cast<float *>(scratch(c, S_ROUTEOUT, routes_n * H * 4, error, capacity));
+    uint32_t *ids = static_cast<uint32_t *>(ctx_scratch(c, S_IDS, std::max<size_t>(T * 8 * 4, 256), error, capacity));
+    float *probs = static_cast<float *>(ctx_scratch(c, S_PROBS, T * 8 * 4, error, capacity));
+    uint32_t *counts = static_cast<uint32_t *>(ctx_scratch(c, S_COUNTS, (size_t)(E + 1) * 4, error, capacity));
+    uint32_t *routes = static_cast<uint32_t *>(ctx_scratch(c, S_ROUTES, (size_t)(E + 1) * T * 4, error, capacity));
+    uint16_t *actb = static_cast<uint16_t *>(ctx_scratch(c, S_ACTBF, routes_n * I * 2, error, capacity));
+    float *rout = static_cast<float *>(ctx_scratch(c, S_ROUTEOUT, routes_n * H * 4, error, capacity));
     if (!ids || !probs || !counts || !routes || !actb || !rout) return -1;
     float *route_out = trace && trace->expert_out ? trace->expert_out : rout;
     hipStream_t s = pick(c, stream);
@@ -985,8 +1101,8 @@ __attribute__((visibility("default"))) int dih_attention(void *ctx, const void *
     a.position = position; a.tokens = tokens; a.partition = part;
     if (nparts > 1) {
         const size_t rows = (size_t)tokens * 16 * nparts;
-        a.pacc = static_cast<float *>(scratch(c, S_APART, rows * 256 * 4, error, capacity));
-        a.pstat = static_cast<float *>(scratch(c, S_ASTAT, rows * 8, error, capacity));
+        a.pacc = static_cast<float *>(ctx_scratch(c, S_APART, rows * 256 * 4, error, capacity));
+        a.pstat = static_cast<float *>(ctx_scratch(c, S_ASTAT, rows * 8, error, capacity));
         if (!a.pacc || !a.pstat) return -1;
     }
     hipStream_t s = pick(c, stream);
@@ -1016,11 +1132,11 @@ __attribute__((visibility("default"))) int dih_delta_rule(void *ctx, float *stat
     a.chunked = path == 0 ? tokens >= kChunkwiseFrom : path == 2;
     if (a.chunked) {
         const size_t blocks = ((size_t)tokens + 31) / 32, tiles = blocks * 32;
-        a.w = static_cast<float *>(scratch(c, S_DW, tiles * 32 * 128 * 4, error, capacity));
-        a.u = static_cast<float *>(scratch(c, S_DU, tiles * 32 * 128 * 4, error, capacity));
-        a.qp = static_cast<float *>(scratch(c, S_DQ, tiles * 32 * 128 * 4, error, capacity));
-        a.cu = static_cast<float *>(scratch(c, S_DCU, tiles * 32 * 128 * 4, error, capacity));
-        a.factors = static_cast<float *>(scratch(c, S_DF, tiles * 32 * 2 * 4, error, capacity));
+        a.w = static_cast<float *>(ctx_scratch(c, S_DW, tiles * 32 * 128 * 4, error, capacity));
+        a.u = static_cast<float *>(ctx_scratch(c, S_DU, tiles * 32 * 128 * 4, error, capacity));
+        a.qp = static_cast<float *>(ctx_scratch(c, S_DQ, tiles * 32 * 128 * 4, error, capacity));
+        a.cu = static_cast<float *>(ctx_scratch(c, S_DCU, tiles * 32 * 128 * 4, error, capacity));
+        a.factors = static_cast<float *>(ctx_scratch(c, S_DF, tiles * 32 * 2 * 4, error, capacity));
         if (!a.w || !a.u || !a.qp || !a.cu || !a.factors) return -1;
     }
     hipStream_t s = pick(c, stream);

@@ -54,6 +54,10 @@ struct Context {
     int prof_used = 0;                        // events taken from the pool since reset
     // named scratch
     Scratch ws[32];
+    // this device's copy of the fixed scratch array of dih_moe_decode_noalloc (its device
+    // address, looked up once per device), or null with the lookup's error
+    void *noalloc = nullptr;
+    std::string noalloc_error;
     uint32_t magic = 0x44494358u;
 };
 
@@ -67,7 +71,7 @@ static_assert(S_COUNT_ <= (int)(sizeof(Context::ws) / sizeof(Scratch)), "scratch
 // Error helpers (bridge.mm:9-15 convention).
 void set_error(char *error, int capacity, const std::string &message);
 bool hip_ok(hipError_t e, char *error, int capacity, const char *what);
-void *scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity);
+void *ctx_scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity);
 bool sync_matrix(Matrix *m, char *error, int capacity);
 
 // Profiling. While a ProfScope for a profiling context is alive on this thread, every

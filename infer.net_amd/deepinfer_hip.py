@@ -82,7 +82,7 @@ EXPORTS = [
     "dih_quant_matrix_commit", "dih_quant_matrix_device", "dih_quant_matrix_shape",
     "dih_quant_batch", "dih_quant_matvec", "dih_quant_experts", "dih_quant_embedding",
     "dih_qmv", "dih_qmv_swiglu", "dih_lm_head", "dih_argmax", "dih_top8", "dih_build_groups",
-    "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm",
+    "dih_dequant_bf16", "dih_moe_decode", "dih_moe_prefill", "dih_moe_decode_norm", "dih_moe_decode_noalloc",
     "dih_moe_prefill_norm", "dih_grouped_qmm", "dih_dense", "dih_attention",
     "dih_attention_partition", "dih_delta_rule", "dih_delta_create", "dih_delta_destroy",
     "dih_delta_step", "dih_set_profiling",
@@ -135,6 +135,7 @@ def load():
         "dih_moe_decode": ([P, P, P, P, P, P, P, E, I], I),
         "dih_moe_prefill": ([P, P, I, P, P, I, P, P, P, E, I], I),
         "dih_moe_decode_norm": ([P, P, P, P, P, P, P, P, E, I], I),
+        "dih_moe_decode_noalloc": ([P, P, P, P, P, P, P, P, E, I], I),
         "dih_moe_prefill_norm": ([P, P, I, P, P, I, P, P, P, P, E, I], I),
         "dih_dense": ([P, P, I, P, P, I, P, E, I], I),
         "dih_grouped_qmm": ([P, P, P, I, P, I, P, P, P, I, P, E, I], I),
@@ -580,6 +581,17 @@ def moe_decode(dev, layer: MoeLayer, x, residual, logits=None, trace: Optional[M
                                         None if merge is None else ctypes.byref(merge),
                                         None if trace is None else ctypes.byref(trace), _stream(stream), err, _ERR),
            err, ArgumentError)
+
+
+def moe_decode_noalloc(dev, layer: MoeLayer, x, residual, logits=None, trace: Optional[MoeTrace] = None,
+                       stream=None, merge: Optional[MoeMerge] = None) -> None:
+    """moe_decode without any device allocation (dih_moe_decode_noalloc): intermediates live
+    in the library's fixed per-GPU scratch array; overlapping calls on one GPU race."""
+    err = _errbuf()
+    _check(dev._lib.dih_moe_decode_noalloc(_ctx(dev), ctypes.byref(layer), _dp(x), _dp(logits), _dp(residual),
+                                           None if merge is None else ctypes.byref(merge),
+                                           None if trace is None else ctypes.byref(trace), _stream(stream), err,
+                                           _ERR), err, ArgumentError)
 
 
 def moe_prefill(dev, layer: MoeLayer, tokens, x, logits, residual, logits_dtype=BF16,

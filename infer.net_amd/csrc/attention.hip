@@ -339,6 +339,7 @@ __global__ __launch_bounds__(512, 1) void attn8_kernel(AttnParams P) {
     __shared__ __align__(16) uint16_t ks[3][kKeys * kDim];
     __shared__ __align__(16) uint16_t vraw[2][kKeys * kDim];
     __shared__ __align__(16) uint16_t vt[2][kDim * kVtStride];
+    lds_escape(ks, vraw, vt);
 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, r = lane & 31, h = lane >> 5;
     // work item: as attn_kernel, with 32-token tiles

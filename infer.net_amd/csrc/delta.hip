@@ -522,6 +522,7 @@ DIH_DEV void apply_block(const ApplySet &S, float (&part)[2][4][2][64 * 4], f4 (
 __global__ __launch_bounds__(512, 1) void delta_apply_kernel(DeltaParams P) {
     __shared__ __align__(16) ApplySet sets[2];
     __shared__ __align__(16) float part[2][4][2][64 * 4];
+    lds_escape(sets, part);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, hl = slot >> 3, rg = slot & 7;
     const int head = 2 * xcd + (hl & 1) + 16 * (hl >> 1), kh = head >> 1;

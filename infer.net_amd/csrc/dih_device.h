@@ -288,6 +288,18 @@ DIH_DEV void wait_lgkm0() { __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8
 
 // Workgroup barrier without a memory fence: __syncthreads() would also wait for every
 // outstanding copy (the fence counts LDS copies as pending stores). Callers first wait
-// for their own copies of the step with wait_vm; the "memory" clobber keeps the compiler
-// from moving LDS accesses across the barrier.
-DIH_DEV void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+// for their own copies of the step with wait_vm. The barrier itself first waits for this
+// wave's LDS reads (lgkmcnt 0): a read still queued at the barrier would race with the
+// copies other waves issue right after it into the buffer being read (write after read),
+// and a copy that hits L2 can land before a read queued behind other waves' LDS traffic.
+// The "memory" clobber keeps the compiler from moving LDS accesses across the barrier,
+// for LDS arrays that have escaped (see lds_escape).
+DIH_DEV void barrier_no_fence() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Makes LDS arrays escape, so that alias analysis treats them as memory that an asm with a
+// "memory" clobber (barrier_no_fence) may touch; without it a __shared__ array that never
+// escapes can have its accesses reordered across such an asm.
+template <typename T>
+DIH_DEV void lds_escape_one(T *p) { asm volatile("" ::"r"(p) : "memory"); }
+template <typename... P>
+DIH_DEV void lds_escape(P... p) { (lds_escape_one(p), ...); }

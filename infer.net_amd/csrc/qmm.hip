@@ -382,11 +382,13 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     // CU when the stages take half of it.
     __shared__ __align__(16) unsigned char st0[ST], st1[ST], st2[ST], st3[ST];
     __shared__ __align__(16) float xch[SPLIT ? 4 * NT * 16 * 64 : 1];
+    lds_escape(st0, st1, st2, st3, xch);
     auto stage_base = [&](int stage) -> unsigned char * {
         return stage == 0 ? st0 : stage == 1 ? st1 : stage == 2 ? st2 : st3;
     };
 
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    // the wave index is uniform: in a scalar register, LDS copy destinations need no readfirstlane
+    const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     const int slab = wave & 3;                // 32-row slab of the 128-row tile
     const int mw = SPLIT ? wave >> 2 : 0;     // split: the matrix this wave computes
     // ---- work item (every wave derives it): physical block b runs logical item
@@ -412,9 +414,16 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
             nrt = min(P.rtb, P.row_tiles - rt0);
         }
     }
+    // the work item is the same in every lane (it came through cross-lane shuffles, which
+    // the compiler cannot see are uniform): keep it in scalar registers so that the step
+    // bookkeeping and the loops over tiles stay scalar
+    e = __builtin_amdgcn_readfirstlane(e);
+    first = __builtin_amdgcn_readfirstlane(first);
+    nvalid = __builtin_amdgcn_readfirstlane(nvalid);
+    rt0 = __builtin_amdgcn_readfirstlane(rt0);
+    nrt = __builtin_amdgcn_readfirstlane(nrt);
     if (rt0 < 0) return;
     const int C = P.columns, R = P.rows, G = C >> 6;
-    const int total_steps = nrt * G;
     // route of the chunk's n-th slot (slots past the chunk repeat its first route)
     auto route_at = [&](int n) -> int {
         n = n < nvalid ? n : 0;
@@ -477,17 +486,41 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
 #pragma unroll
     for (int i = 0; i < NT; i++) out_route[i] = route_at(32 * i + r);
 
-    // copies of flattened step s (row tile s / G, K step s % G) into `stage`
-    auto issue = [&](int step, int stage) {
-        step = step < total_steps ? step : total_steps - 1;
-        const int ti = step / G, kg = step - ti * G;
+    // Copy sources: the expert's first row in each matrix (wave-uniform) plus a 32-bit lane
+    // offset of the row within the expert (an expert's rows span less than 2^31 bytes, checked
+    // on the host); a K step adds the wave-uniform offset kg * AB. The issue position (the
+    // next step to copy, as tile and K step) is wave-uniform, so the step bookkeeping is scalar
+    // and no step index is divided at run time.
+    const char *wbase[WMAT];
+#pragma unroll
+    for (int mm = 0; mm < WMAT; mm++) wbase[mm] = pw[mm + mw] + ebase * row_bytes;
+    uint32_t woff[AQ];
+    auto set_tile = [&](int ti) {
+#pragma unroll
+        for (int q = 0; q < AQ; q++) {
+            const int row = (rt0 + ti) * TR + crow[q];
+            woff[q] = (uint32_t)((row < R ? row : R - 1) * (uint32_t)row_bytes) + (uint32_t)coff[q];
+        }
+    };
+    int iss_ti = 0, iss_kg = 0;
+    set_tile(0);
+    // copies step (iss_ti, iss_kg) into `stage`, then moves to the next step; past the last
+    // step the last one is copied again
+    auto issue = [&](int stage) {
         unsigned char *base = stage_base(stage);
+        // The lane offsets are recomputed at every step (a few VALU operations a copy) rather
+        // than held across steps. With them held, the copies issued nearly back to back and,
+        // in some builds, one 32-route activation tile of every chunk never received its data
+        // on gfx950 (which kernels failed moved with the schedule; the cause was not found).
+        // With the address arithmetic between the copies every build passed the parity tests.
+        set_tile(iss_ti);
+        const uint32_t koff = (uint32_t)iss_kg * AB;
 #pragma unroll
         for (int mm = 0; mm < WMAT; mm++) {
             const int m = mm + mw;
 #pragma unroll
             for (int q = 0; q < AQ; q++) {
-                const char *src = pw[m] + row_index(rt0 + ti, crow[q]) * row_bytes + (size_t)kg * AB + coff[q];
+                const char *src = wbase[mm] + (woff[q] + koff);
                 if constexpr (BITS == 8)
                     to_lds<16>(src, base + m * A_ST + (slab * 32 * RS + 16 * q) * 64);
                 else
@@ -495,11 +528,17 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
             }
         }
 #pragma unroll
-        for (int i = 0; i < NBW; i++) to_lds<16>(bsrc[i] + 64 * kg, base + NMAT * A_ST + (NW * i + wave) * 8 * 128);
+        for (int i = 0; i < NBW; i++) to_lds<16>(bsrc[i] + 64 * iss_kg, base + NMAT * A_ST + (NW * i + wave) * 8 * 128);
+        if (iss_kg + 1 < G) {
+            iss_kg++;
+        } else if (iss_ti + 1 < nrt) {
+            iss_ti++;
+            iss_kg = 0;
+        }
     };
 
 #pragma unroll
-    for (int st = 0; st < S - 1; st++) issue(st, st);
+    for (int st = 0; st < S - 1; st++) issue(st);
     u32x4 win[RS][2][2], win_next[RS][2][2];
     win_load(win, 0, 0);
 
@@ -529,10 +568,9 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
             if (more) win_load(win_next, kw + 8 < G ? ti : ti + 1, kw + 8 < G ? (kw >> 3) + 1 : 0);
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int step = ti * G + kw + u;
                 wait_vm<(S - 2) * LPS>();
                 barrier_no_fence();
-                issue(step + S - 1, (u + S - 1) % S);
+                issue((u + S - 1) % S);
                 const unsigned char *base = stage_base(u % S);
                 // this step's weights -> bf16 A operands (a[rs * WMAT + m]: slab rs, matrix m)
                 dih_bf16x8 a[RS * 2][4];
@@ -672,6 +710,11 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     P.x = a.x; P.y = a.y;
     if (!a.dense && (a.ngroups < 1 || a.ngroups > 320 || !a.routes || !a.counts)) {
         set_error(error, capacity, "Invalid grouped qmm arguments");
+        return false;
+    }
+    // the streaming kernel addresses an expert's weight rows with 32-bit offsets
+    if ((size_t)m0->rows * ((size_t)m0->columns * m0->bits / 8) > 0x7fffffffu) {
+        set_error(error, capacity, "Matrix too large for one grouped/dense qmm launch");
         return false;
     }
     // input row offsets (row * columns) are 32-bit in the kernel

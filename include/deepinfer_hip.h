@@ -283,10 +283,14 @@ int dih_dense(void *context, void *matrix, int tokens, const void *x, void *y, i
  *           sit at h*512+256 .. h*512+511
  *   out     [tokens][16][256] f32 or bf16:
  *           softmax(q.k/16 over keys 0..position+t) . v * sigmoid(gate)
- *   partition  keys per partition, a multiple of 32; 0 lets the library choose (32 for one
- *           token, which runs the decode kernel). Keys are scanned in 32-key blocks;
- *           probabilities are rounded to bf16 per block against the running maximum of
- *           their partition, as the reference rounds them.
+ *   partition  the rounding partition: keys 0.., partition.., 2*partition.. whose
+ *           probabilities are rounded against one running maximum; a multiple of 32, 0 for
+ *           the reference's default of 1024 (attentionPartitionTokens, gpu_prefill.mm:393,
+ *           486-489, 554). Keys are scanned in 32-key blocks; each block's probabilities are
+ *           rounded to bf16 against the running maximum of its partition through that block,
+ *           as the reference rounds them. 32 makes every block its own partition, the
+ *           fastest decode form. How the keys are split over the GPU is the library's choice
+ *           and does not change the rounding points.
  * Device pointers; runs on `stream` (NULL: the context's stream). Returns 0, or -1 with a
  * message when an argument is invalid (nothing is launched then). */
 int dih_attention(void *context, const void *q, int q_dtype, const uint16_t *keys,
@@ -294,12 +298,8 @@ int dih_attention(void *context, const void *q, int q_dtype, const uint16_t *key
                   void *out, int out_dtype, int position, int tokens, int partition,
                   void *stream, char *error, int capacity);
 
-/* The partition size dih_attention uses for these arguments (`partition` itself when it
- * is positive, else the library's choice); -1 for invalid arguments. The partition sets
- * where probabilities are rounded (see dih_attention) and the partial-result scratch:
- * tokens * 16 * ceil((position + tokens) / partition) * 1032 bytes when above one (one
- * token with 32-key partitions: 16 * ceil((position + 1) / 128) * 1032 bytes, the decode
- * kernel merging four partitions a block). */
+/* The rounding partition dih_attention uses for these arguments (`partition` itself when
+ * it is positive, else 1024); -1 for invalid arguments. */
 int dih_attention_partition(int position, int tokens, int partition);
 
 /* Gated delta rule of a linear-attention (Gated DeltaNet) layer over a chunk of `tokens`

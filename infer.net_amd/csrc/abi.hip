@@ -1091,19 +1091,24 @@ __attribute__((visibility("default"))) int dih_attention(void *ctx, const void *
         set_error(error, capacity, "Invalid attention arguments");
         return -1;
     }
-    const int part = attention_partition(position, tokens, partition);
+    const int round = attention_partition(position, tokens, partition);
+    const int part = attention_split(position, tokens, round);
     const size_t nparts = (size_t)attention_partials(position, tokens, part);
     AttentionArgs a;
     a.q = q; a.q_bf16 = q_dtype == DIH_BF16;
     a.keys = keys; a.values = values;
     a.gate = gate; a.gate_bf16 = gate_dtype == DIH_BF16;
     a.out = out; a.out_bf16 = out_dtype == DIH_BF16;
-    a.position = position; a.tokens = tokens; a.partition = part;
+    a.position = position; a.tokens = tokens; a.partition = part; a.round = round;
     if (nparts > 1) {
         const size_t rows = (size_t)tokens * 16 * nparts;
         a.pacc = static_cast<float *>(ctx_scratch(c, S_APART, rows * 256 * 4, error, capacity));
         a.pstat = static_cast<float *>(ctx_scratch(c, S_ASTAT, rows * 8, error, capacity));
         if (!a.pacc || !a.pstat) return -1;
+    }
+    if (const size_t sf = attention_score_floats(position, tokens, round, part)) {
+        a.scores = static_cast<float *>(ctx_scratch(c, S_ASCORE, sf * 4, error, capacity));
+        if (!a.scores) return -1;
     }
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(c);

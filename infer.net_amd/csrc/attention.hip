@@ -48,6 +48,9 @@ struct AttnParams {
     float *pacc;       // [token][16][nparts][256] unnormalized partition outputs (split only)
     float2 *pstat;     // [token][16][nparts] (max in log2 units, sum)
     int position, tokens, partition, nparts, ntiles;
+    int round;         // keys per rounding partition (a multiple of 32 dividing `partition`)
+    float *scores;     // decode with rounding partitions: [2][tiles][32 lanes][8] raw scores
+    float *tmax;       // and [2][tiles][8] tile maxima (log2 units)
 };
 
 DIH_DEV float sigmoid_f(float g) { return 1.f / (1.f + __expf(-g)); }
@@ -176,12 +179,36 @@ DIH_DEV void load_queries(dih_bf16x8 (&qreg)[16], const AttnParams &P, int my_to
     }
 }
 
+// A row's softmax state over the keys a block scans. Probabilities are rounded against
+// `m`, the running maximum of the current rounding partition (restarted at its first key),
+// and the accumulators and `sum` are kept in the scale 2^-(m + ak). Normally ak = 0: the
+// accumulators follow the rounding maximum, and after a restart (a partition whose maximum
+// is below an earlier one) they are scaled up by 2^(old - new) rather than the new
+// partition's probabilities being scaled down, which keeps the bf16 probabilities exactly as
+// rounded. Only when that would put the scale more than 2^kMaxUp below `seen` (the maximum
+// of every key scanned; accumulators near 2^(15 + kMaxUp) times the largest value) does ak
+// rise, and the partition's probabilities enter scaled by the exact power of two 2^-ak. All
+// maxima are in log2 units (score * log2(e) / 16).
+constexpr float kMaxUp = 64.f;
+struct RowState {
+    float m = -INFINITY, seen = -INFINITY, ak = 0.f, sum = 0.f;
+    DIH_DEV float scale_max() const { return m == -INFINITY ? -INFINITY : m + ak; }
+};
+
+// bf16 pair `w` times the power of two `f` (exact: only the exponents change, values below
+// the normal range excepted, which are negligible next to the row's sum).
+DIH_DEV uint32_t scale_bf16x2(uint32_t w, float f) {
+    return pack_bf16x2(__uint_as_float(w << 16) * f, __uint_as_float(w & 0xffff0000u) * f);
+}
+
 // One 32-key tile (keys kb.., rows from ksb, values transposed in vtb) for the wave's rows.
-// `full`: every row of the wave sees the whole tile (no mask needed).
+// `full`: every row of the wave sees the whole tile (no mask needed). RESTARTS: the block's
+// keys span more than one rounding partition; `restart`: this tile starts one (and is not
+// the block's first tile).
+template <bool RESTARTS>
 DIH_DEV void attend_tile(const uint16_t *ksb, const uint16_t *vtb, const dih_bf16x8 (&qreg)[16],
-                         dih_f32x16 (&acc)[8], float &m_run, float &l_run, int kb, int kend, bool full,
-                         int my_last, int r, int h) {
-    // ---- S^T = K Q^T: s[k] is key kb + 8(k/4) + 4h + k%4 of row r
+                         dih_f32x16 (&acc)[8], RowState &st, int kb, int kend, bool full, bool restart,
+                         int my_last, int r, int h) {    // ---- S^T = K Q^T: s[k] is key kb + 8(k/4) + 4h + k%4 of row r
     dih_f32x16 s;
 #pragma unroll
     for (int k = 0; k < 16; k++) s[k] = 0.f;
@@ -205,9 +232,24 @@ DIH_DEV void attend_tile(const uint16_t *ksb, const uint16_t *vtb, const dih_bf1
         }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx * kLog2eOver16);
-    const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;   // all keys masked so far: p = 0
+    const float tmax = mx * kLog2eOver16;
+    float r_new, alpha, f = 1.f;
+    if constexpr (RESTARTS) {
+        // a row with no visible key in this tile has none in any later one (causal and kend
+        // masks only grow): it keeps its maximum, its p are 0 and alpha is 1
+        r_new = restart && tmax != -INFINITY ? tmax : fmaxf(st.m, tmax);
+        const float seen = fmaxf(st.seen, tmax);
+        const float k_new = fmaxf(ceilf(seen - r_new) - kMaxUp, 0.f);   // (NaN: nothing seen -> 0)
+        alpha = st.m == -INFINITY ? 0.f : exp2f((st.m - r_new) + (st.ak - k_new));
+        f = __builtin_amdgcn_ldexpf(1.f, -(int)k_new);
+        st.seen = seen;
+        st.ak = k_new;
+    } else {
+        r_new = fmaxf(st.m, tmax);
+        alpha = st.m == -INFINITY ? 0.f : exp2f(st.m - r_new);
+    }
+    st.m = r_new;
+    const float m_use = r_new == -INFINITY ? 0.f : r_new;   // all keys masked: p = 0
     float psum = 0.f;
     uint32_t pw[8];
 #pragma unroll
@@ -218,9 +260,13 @@ DIH_DEV void attend_tile(const uint16_t *ksb, const uint16_t *vtb, const dih_bf1
         pw[k >> 1] = pack_bf16x2(p0, p1);
     }
     psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // rescale only when some row's maximum moved (alpha == 1 exactly otherwise)
+    st.sum = st.sum * alpha + psum * f;
+    // probabilities of a partition far below the scale: rounded above, then scaled exactly
+    if (RESTARTS && __ballot(f != 1.f)) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) pw[i] = scale_bf16x2(pw[i], f);
+    }
+    // rescale only when some row's scale moved (alpha == 1 exactly otherwise)
     if (__ballot(alpha != 1.f)) {
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
@@ -246,10 +292,10 @@ DIH_DEV void attend_tile(const uint16_t *ksb, const uint16_t *vtb, const dih_bf1
 
 // The wave's rows after the partition: the output itself, or the partition's statistics
 // and unnormalized values for the combine.
-DIH_DEV void finish_rows(const AttnParams &P, const dih_f32x16 (&acc)[8], float m_run, float l_run, int my_tok,
+DIH_DEV void finish_rows(const AttnParams &P, const dih_f32x16 (&acc)[8], const RowState &st, int my_tok,
                          int head, int part, int h) {
     if (P.nparts == 1) {
-        const float inv = 1.f / l_run;
+        const float inv = 1.f / st.sum;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
 #pragma unroll
@@ -259,7 +305,7 @@ DIH_DEV void finish_rows(const AttnParams &P, const dih_f32x16 (&acc)[8], float 
             }
     } else {
         const size_t pi = ((size_t)my_tok * kHeads + head) * P.nparts + part;
-        if (h == 0) P.pstat[pi] = make_float2(m_run, l_run);
+        if (h == 0) P.pstat[pi] = make_float2(st.scale_max(), st.sum);
         float *pa = P.pacc + pi * kDim;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
@@ -270,6 +316,7 @@ DIH_DEV void finish_rows(const AttnParams &P, const dih_f32x16 (&acc)[8], float 
     }
 }
 
+template <bool RESTARTS>
 __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
     __shared__ __align__(16) uint16_t ks[2][kKeys * kDim];
     __shared__ __align__(16) uint16_t vraw[kKeys * kDim];
@@ -302,7 +349,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
     // ---- tiles are copied one compute phase ahead
     const uint16_t *kbase = P.keys + kh * kDim, *vbase = P.values + kh * kDim;
     const int vq = t & 7, vc = t >> 3;
-    float m_run = -INFINITY, l_run = 0.f;
+    RowState st;
     dih_f32x16 acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
@@ -323,10 +370,11 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
         }
         if (!wave_ok || kb > wave_last) continue;
         const bool full = kb + kKeys - 1 <= P.position + wtok0 && kb + kKeys <= kend;
-        attend_tile(ks[buf], vt, qreg, acc, m_run, l_run, kb, kend, full, my_last, r, h);
+        attend_tile<RESTARTS>(ks[buf], vt, qreg, acc, st, kb, kend, full,
+                              RESTARTS && kb != kstart && kb % P.round == 0, my_last, r, h);
     }
     if (!row_ok) return;
-    finish_rows(P, acc, m_run, l_run, my_tok, head, part, h);
+    finish_rows(P, acc, st, my_tok, head, part, h);
 }
 
 // ---- eight-wave form: 32 query tokens (256 rows) per block share each key/value tile.
@@ -335,6 +383,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnParams P) {
 //   top of tile j: tile j's keys and transposed values are in LDS, tile j+1's copies landed
 //   issue tile j+2's copies (into the buffers tile j-1 used), compute tile j, transpose
 //   tile j+1's values, wait for this thread's copies, barrier.
+template <bool RESTARTS>
 __global__ __launch_bounds__(512, 1) void attn8_kernel(AttnParams P) {
     __shared__ __align__(16) uint16_t ks[3][kKeys * kDim];
     __shared__ __align__(16) uint16_t vraw[2][kKeys * kDim];
@@ -362,7 +411,7 @@ __global__ __launch_bounds__(512, 1) void attn8_kernel(AttnParams P) {
 
     dih_bf16x8 qreg[16];
     load_queries(qreg, P, my_tok, row_ok, head, h);
-    float m_run = -INFINITY, l_run = 0.f;
+    RowState st;
     dih_f32x16 acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
@@ -396,7 +445,8 @@ __global__ __launch_bounds__(512, 1) void attn8_kernel(AttnParams P) {
         }
         if (wave_ok && kb <= wave_last) {
             const bool full = kb + kKeys - 1 <= P.position + wtok0 && kb + kKeys <= kend;
-            attend_tile(ks[k3], vt[j & 1], qreg, acc, m_run, l_run, kb, kend, full, my_last, r, h);
+            attend_tile<RESTARTS>(ks[k3], vt[j & 1], qreg, acc, st, kb, kend, full,
+                                  RESTARTS && kb != kstart && kb % P.round == 0, my_last, r, h);
         }
         if (j + 1 < ntile) transpose_values8(vraw[(j + 1) & 1], vt[(j + 1) & 1], t);
         wait_vm<0>();
@@ -405,7 +455,7 @@ __global__ __launch_bounds__(512, 1) void attn8_kernel(AttnParams P) {
         k3 = k3 == 2 ? 0 : k3 + 1;
     }
     if (!row_ok) return;
-    finish_rows(P, acc, m_run, l_run, my_tok, head, part, h);
+    finish_rows(P, acc, st, my_tok, head, part, h);
 }
 
 // One wave per (token, head), four dims per lane: merge the partitions that hold keys of
@@ -465,12 +515,89 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams P) {
 // Products are v_mfma_f32_16x16x32_bf16 (lane l: row l % 16, k = 8(l / 16)..+7; result
 // rows 4(l / 16) + i).
 constexpr int kDecKeys = 4 * kKeys;   // keys per decode block
+// the reference's default rounding partition (attentionPartitionTokens, gpu_prefill.mm:393)
+constexpr int kDefaultRound = 1024;
+// longest rounding partition the decode scores pass serves (a lane reads a quarter of its
+// tile maxima: 32 at most); longer ones run the general kernel
+constexpr int kMaxPremaxRound = 4096;
 
 DIH_DEV dih_f32x4 mfma16_bf16(dih_bf16x8 a, dih_bf16x8 b, dih_f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Decode with rounding partitions longer than a tile (PREMAX): attn_decode_scores_kernel
+// first writes every tile's raw scores and per-row maxima; the decode kernel then takes its
+// tile's scores from there and rounds the probabilities against the running maximum of the
+// rounding partition up to and including its tile (the maxima of that partition's earlier
+// tiles, read back), which is the reference's rounding point, while the blocks still split
+// the keys 128 at a time.
+//
+// Scores kernel: the same block and wave mapping as the decode kernel. Lane (n < 8, g) of a
+// tile's wave stores s[mt][i] (key kb + 16mt + 4g + i, head 8kh + n) at
+// scores[((kh * tiles + tile) * 32 + 8g + n) * 8 + 4mt + i] and lane (n, 0) the row maximum
+// at tmax[(kh * tiles + tile) * 8 + n]; masked keys are -inf.
 template <bool QBF16>
+__global__ __launch_bounds__(256) void attn_decode_scores_kernel(AttnParams P) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, n = lane & 15, g = lane >> 4;
+    const int b = blockIdx.x, x = b & 7, kh = x >> 2;
+    const int idx = (x & 3) + 4 * (b >> 3);
+    if (idx >= P.nparts) return;   // whole block
+    const int kend = P.position + 1;
+    const int kb = idx * kDecKeys + kKeys * wave;
+    const uint16_t *kbase = P.keys + kh * kDim;
+    dih_bf16x8 ka[2][8];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        const uint32_t key = (uint32_t)min(kb + 16 * mt + n, kend - 1);
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            ka[mt][s] = *reinterpret_cast<const dih_bf16x8 *>(kbase + key * (uint32_t)(kKvHeads * kDim) + 32 * s + 8 * g);
+    }
+    const int qhead = kh * kGroup + (n & 7);
+    dih_bf16x8 qb[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        uint4 u = make_uint4(0, 0, 0, 0);
+        if (n < kGroup) {
+            if constexpr (QBF16) {
+                u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(P.q) + (size_t)qhead * kDim + 32 * s + 8 * g);
+            } else {
+                const float *qs = static_cast<const float *>(P.q) + (size_t)qhead * kDim + 32 * s + 8 * g;
+                const float4 f0 = *reinterpret_cast<const float4 *>(qs), f1 = *reinterpret_cast<const float4 *>(qs + 4);
+                u.x = pack_bf16x2(f0.x, f0.y); u.y = pack_bf16x2(f0.z, f0.w);
+                u.z = pack_bf16x2(f1.x, f1.y); u.w = pack_bf16x2(f1.z, f1.w);
+            }
+        }
+        qb[s] = __builtin_bit_cast(dih_bf16x8, u);
+    }
+    dih_f32x4 sc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        sc[mt] = dih_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; s++) sc[mt] = mfma16_bf16(ka[mt][s], qb[s], sc[mt]);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = kb + 16 * mt + 4 * g + i;
+            sc[mt][i] = key < kend ? sc[mt][i] : -INFINITY;
+            mx = fmaxf(mx, sc[mt][i]);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (n < kGroup) {
+        const size_t ti = (size_t)kh * (4 * P.nparts) + 4 * idx + wave;
+        float4 *dst = reinterpret_cast<float4 *>(P.scores + (ti * 32 + 8 * g + n) * 8);
+        dst[0] = make_float4(sc[0][0], sc[0][1], sc[0][2], sc[0][3]);
+        dst[1] = make_float4(sc[1][0], sc[1][1], sc[1][2], sc[1][3]);
+        if (g == 0) P.tmax[ti * 8 + n] = mx * kLog2eOver16;
+    }
+}
+
+template <bool QBF16, bool PREMAX>
 __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
     __shared__ __align__(16) uint16_t vt[4][kDim * kVtStride];   // per wave; its partial sums after
     __shared__ __align__(16) uint16_t pb[4][16 * kKeys];         // per wave: bf16 probabilities [row][key]
@@ -487,12 +614,14 @@ __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
     // keys, the A operand: m-tile mt, k-step s: key kb + 16mt + n, dims 32s + 8g..+7
     // (indices past the visible keys clamped to the last one; those scores are masked)
     dih_bf16x8 ka[2][8];
+    if constexpr (!PREMAX) {
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-        const uint32_t key = (uint32_t)min(kb + 16 * mt + n, kend - 1);
+        for (int mt = 0; mt < 2; mt++) {
+            const uint32_t key = (uint32_t)min(kb + 16 * mt + n, kend - 1);
 #pragma unroll
-        for (int s = 0; s < 8; s++)
-            ka[mt][s] = *reinterpret_cast<const dih_bf16x8 *>(kbase + key * (uint32_t)(kKvHeads * kDim) + 32 * s + 8 * g);
+            for (int s = 0; s < 8; s++)
+                ka[mt][s] = *reinterpret_cast<const dih_bf16x8 *>(kbase + key * (uint32_t)(kKvHeads * kDim) + 32 * s + 8 * g);
+        }
     }
     // values for the transpose: keys kb + 4vq + i, dims 8vc..8vc+7, vc = lane / 8 + 8j
     const int vq = lane & 7;
@@ -508,10 +637,26 @@ __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
     // 8kh + n (rows 8..15 zero); loaded raw behind the keys and values, converted after, so
     // that all of the wave's loads are in flight together
     const int qhead = kh * kGroup + (n & 7);
+    // PREMAX: the tile's scores (rows 8..15: none, -inf) and the rounding maximum, the
+    // largest of the tile maxima from the rounding partition's first tile through this one
+    // (lane (n, g) reads every fourth of them, then the four lanes of row n combine)
+    float4 sv[2] = {make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY),
+                    make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY)};
+    float rmax = -INFINITY;
+    if constexpr (PREMAX) {
+        if (n < kGroup) {
+            const size_t ti0 = (size_t)kh * (4 * P.nparts);
+            const int tile = 4 * idx + wave, first = tile - tile % (P.round / kKeys);
+            const float4 *src = reinterpret_cast<const float4 *>(P.scores + ((ti0 + tile) * 32 + 8 * g + n) * 8);
+            sv[0] = src[0];
+            sv[1] = src[1];
+            for (int tt = first + g; tt <= tile; tt += 4) rmax = fmaxf(rmax, P.tmax[(ti0 + tt) * 8 + n]);
+        }
+    }
     // (rows 8..15 load nothing: a branch, so that their lanes are off for the loads)
     float4 qf[8][2] = {};
     uint4 qu[8] = {};
-    if (n < kGroup) {
+    if (!PREMAX && n < kGroup) {
         if constexpr (QBF16) {
             const uint16_t *qs = static_cast<const uint16_t *>(P.q) + (size_t)qhead * kDim + 8 * g;
 #pragma unroll
@@ -540,11 +685,16 @@ __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
 
     // ---- S = K Q^T: s[mt][i] is key kb + 16mt + 4g + i of row n
     dih_f32x4 sc[2];
+    if constexpr (PREMAX) {
+        sc[0] = dih_f32x4{sv[0].x, sv[0].y, sv[0].z, sv[0].w};
+        sc[1] = dih_f32x4{sv[1].x, sv[1].y, sv[1].z, sv[1].w};
+    } else {
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-        sc[mt] = dih_f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < 2; mt++) {
+            sc[mt] = dih_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 8; s++) sc[mt] = mfma16_bf16(ka[mt][s], qb[s], sc[mt]);
+            for (int s = 0; s < 8; s++) sc[mt] = mfma16_bf16(ka[mt][s], qb[s], sc[mt]);
+        }
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -555,9 +705,10 @@ __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
             sc[mt][i] = key < kend ? sc[mt][i] : -INFINITY;
             mx = fmaxf(mx, sc[mt][i]);
         }
+    if constexpr (PREMAX) mx = rmax;   // the rounding maximum is in log2 units already
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = mx * kLog2eOver16;
+    const float m_new = PREMAX ? mx : mx * kLog2eOver16;
     const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a tile past the keys: p = 0
     float psum = 0.f;
     uint16_t *pbw = pb[wave];
@@ -721,35 +872,51 @@ __global__ __launch_bounds__(256) void attn_combine_wide_kernel(AttnParams P) {
 static bool wide_blocks(int tokens) { return tokens > 2 * kTok; }
 
 int attention_partition(int position, int tokens, int requested) {
-    if (requested > 0) return requested;
-    // one decode token: 32-key partitions (attn_decode_kernel)
-    if (tokens == 1) return kKeys;
+    (void)position; (void)tokens;
+    return requested > 0 ? requested : kDefaultRound;
+}
+
+int attention_split(int position, int tokens, int round) {
+    // one decode token: the decode kernels (128-key blocks of 32-key tiles); their own
+    // rounding when the partition is one tile, else the scores pass first
+    if (tokens == 1 && (round == kKeys || (round % kDecKeys == 0 && round <= kMaxPremaxRound))) return kKeys;
     const bool wide = wide_blocks(tokens);
     const int tile_tokens = wide ? 2 * kTok : kTok;
     const int ntiles = (tokens + tile_tokens - 1) / tile_tokens;
     const int keys = position + tokens;
+    int part;
     if (ntiles == 1) {
-        // decode / short chunks: the key stream is latency-bound; about 128 partitions per
-        // KV head of at least 128 keys (measured best at 8K and 32K positions)
-        const int part = (((keys + 127) / 128) + 127) / 128 * 128;
-        return part < 128 ? 128 : part;
+        // short chunks: the key stream is latency-bound; about 128 partitions per KV head
+        // of at least 128 keys (measured best at 8K and 32K positions)
+        part = std::max(128, (((keys + 127) / 128) + 127) / 128 * 128);
+    } else {
+        // (tile, KV head, partition) items: eight-wave blocks, one resident per CU, take one
+        // round of the 256-CU part (measured at 16K and 32K positions: 8 partitions of 4096
+        // keys 1.33 ms, 4 of 8192 1.19 ms, 2 of 16384 1.12 ms for the last 2048-token chunk
+        // of a 32K prompt); four-wave blocks two per CU, more when the keys are long
+        const int items = ntiles * kKvHeads;
+        const int target = wide ? 256 : 512 * std::min(4, std::max(1, keys / 8192));
+        if (items >= target) {
+            part = ((keys + kKeys - 1) / kKeys) * kKeys;
+        } else {
+            const int parts = (target + items - 1) / items;
+            part = std::max(256, ((keys + parts - 1) / parts + 255) / 256 * 256);
+        }
     }
-    // (tile, KV head, partition) items: eight-wave blocks, one resident per CU, take one
-    // round of the 256-CU part (measured at 16K and 32K positions: 8 partitions of 4096
-    // keys 1.33 ms, 4 of 8192 1.19 ms, 2 of 16384 1.12 ms for the last 2048-token chunk of
-    // a 32K prompt); four-wave blocks two per CU, more when the keys are long
-    const int items = ntiles * kKvHeads;
-    const int target = wide ? 256 : 512 * std::min(4, std::max(1, keys / 8192));
-    if (items >= target) return ((keys + kKeys - 1) / kKeys) * kKeys;
-    const int parts = (target + items - 1) / items;
-    int part = (keys + parts - 1) / parts;
-    part = ((part + 255) / 256) * 256;
-    return part < 256 ? 256 : part;
+    // work partitions hold whole rounding partitions (one partition may cover every key)
+    if (part >= keys) return ((keys + kKeys - 1) / kKeys) * kKeys;
+    return (part + round - 1) / round * round;
 }
 
 int attention_partials(int position, int tokens, int partition) {
     if (tokens == 1 && partition == kKeys) return (position + kDecKeys) / kDecKeys;   // decode blocks
     return (position + tokens + partition - 1) / partition;
+}
+
+size_t attention_score_floats(int position, int tokens, int round, int partition) {
+    if (tokens != 1 || partition != kKeys || round == kKeys) return 0;
+    const size_t tiles = 4 * (size_t)attention_partials(position, tokens, partition);
+    return kKvHeads * tiles * (32 * 8 + 8);
 }
 
 bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity) {
@@ -759,8 +926,14 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
     P.gate = a.gate; P.gate_bf16 = a.gate_bf16;
     P.out = a.out; P.out_bf16 = a.out_bf16;
     P.pacc = a.pacc; P.pstat = reinterpret_cast<float2 *>(a.pstat);
-    P.position = a.position; P.tokens = a.tokens; P.partition = a.partition;
+    P.position = a.position; P.tokens = a.tokens; P.partition = a.partition; P.round = a.round;
+    P.scores = a.scores; P.tmax = nullptr;
     P.nparts = attention_partials(a.position, a.tokens, a.partition);
+    if (P.round < kKeys || P.round % kKeys != 0 || (a.partition != kKeys && a.partition % P.round != 0 &&
+                                                    a.partition < a.position + a.tokens)) {
+        set_error(error, capacity, "Attention work partitions must hold whole rounding partitions");
+        return false;
+    }
     const bool wide = wide_blocks(a.tokens);
     P.ntiles = (a.tokens + (wide ? 2 * kTok : kTok) - 1) / (wide ? 2 * kTok : kTok);
     if (P.nparts > 1 && (!P.pacc || !P.pstat)) {
@@ -768,15 +941,34 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
         return false;
     }
     if (a.tokens == 1 && a.partition == kKeys) {
-        // decode: four 32-key partitions a block, merged there; the blocks' partial results
-        // are combined by (token, head, 32 dims)
+        // decode: four 32-key tiles a block, merged there; the blocks' partial results are
+        // combined by (token, head, 32 dims)
         P.partition = kDecKeys;
-        prof_stage("attention");
         const dim3 grid(2 * ((P.nparts + 3) / 4 * 4));
-        if (P.q_bf16)
-            DIH_LAUNCH(attn_decode_kernel<true>, grid, dim3(256), 0, s, P);
-        else
-            DIH_LAUNCH(attn_decode_kernel<false>, grid, dim3(256), 0, s, P);
+        if (P.round != kKeys) {
+            if (!P.scores) {
+                set_error(error, capacity, "Decode attention with rounding partitions needs a score buffer");
+                return false;
+            }
+            P.tmax = P.scores + (size_t)kKvHeads * 4 * P.nparts * 32 * 8;
+            prof_stage("attention_scores");
+            if (P.q_bf16)
+                DIH_LAUNCH(attn_decode_scores_kernel<true>, grid, dim3(256), 0, s, P);
+            else
+                DIH_LAUNCH(attn_decode_scores_kernel<false>, grid, dim3(256), 0, s, P);
+            if (!hip_ok(hipGetLastError(), error, capacity, "attention scores launch")) return false;
+        }
+        prof_stage("attention");
+        if (P.round != kKeys) {
+            if (P.q_bf16)
+                DIH_LAUNCH((attn_decode_kernel<true, true>), grid, dim3(256), 0, s, P);
+            else
+                DIH_LAUNCH((attn_decode_kernel<false, true>), grid, dim3(256), 0, s, P);
+        } else if (P.q_bf16) {
+            DIH_LAUNCH((attn_decode_kernel<true, false>), grid, dim3(256), 0, s, P);
+        } else {
+            DIH_LAUNCH((attn_decode_kernel<false, false>), grid, dim3(256), 0, s, P);
+        }
         if (!hip_ok(hipGetLastError(), error, capacity, "attention launch")) return false;
         if (P.nparts > 1) {
             prof_stage("attention_combine");
@@ -786,11 +978,17 @@ bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int ca
         return true;
     }
     const int per = ((P.ntiles * P.nparts + 3) / 4) * 4;
+    // blocks whose keys span one rounding partition run the plain online softmax
+    const bool restarts = P.partition > P.round;
     prof_stage("attention");
-    if (wide)
-        DIH_LAUNCH(attn8_kernel, dim3(2 * per), dim3(512), 0, s, P);
+    if (wide && restarts)
+        DIH_LAUNCH(attn8_kernel<true>, dim3(2 * per), dim3(512), 0, s, P);
+    else if (wide)
+        DIH_LAUNCH(attn8_kernel<false>, dim3(2 * per), dim3(512), 0, s, P);
+    else if (restarts)
+        DIH_LAUNCH(attn_kernel<true>, dim3(2 * per), dim3(256), 0, s, P);
     else
-        DIH_LAUNCH(attn_kernel, dim3(2 * per), dim3(256), 0, s, P);
+        DIH_LAUNCH(attn_kernel<false>, dim3(2 * per), dim3(256), 0, s, P);
     if (!hip_ok(hipGetLastError(), error, capacity, "attention launch")) return false;
     if (P.nparts > 1) {
         prof_stage("attention_combine");

@@ -64,7 +64,7 @@ struct Context {
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_COUNT_
 };
 static_assert(S_COUNT_ <= (int)(sizeof(Context::ws) / sizeof(Scratch)), "scratch table too small");
 
@@ -215,13 +215,20 @@ struct AttentionArgs {
     const void *gate = nullptr; int gate_bf16 = 0;
     void *out = nullptr; int out_bf16 = 0;
     float *pacc = nullptr; float *pstat = nullptr;
-    int position = 0, tokens = 0, partition = 0;
+    float *scores = nullptr;   // decode with rounding partitions: attention_score_floats floats
+    int position = 0, tokens = 0, partition = 0, round = 0;
 };
-// Partition size for a call: `requested` when positive, else enough partitions that the
-// blocks fill the GPU.
+// Rounding partition of a call (keys whose probabilities are rounded against one running
+// maximum): `requested` when positive, else the reference's 1024.
 int attention_partition(int position, int tokens, int requested);
-// Partial-result slots per (token, head) a call with that partition writes (1: none).
+// Work partition (keys one block scans) for that rounding partition: whole rounding
+// partitions, enough of them that the blocks fill the GPU; 32 for one decode token on the
+// decode kernels.
+int attention_split(int position, int tokens, int round);
+// Partial-result slots per (token, head) a call with that work partition writes (1: none).
 int attention_partials(int position, int tokens, int partition);
+// Floats of score scratch the decode scores pass needs (0: none).
+size_t attention_score_floats(int position, int tokens, int round, int partition);
 bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity);
 
 // Gated delta rule over a chunk (delta.hip): state [32][128][128] f32 and history

@@ -622,7 +622,9 @@ def dense(dev, m, tokens, x, y, y_dtype=F32, stream=None) -> None:
 def attention(dev, q, keys, values, gate, out, position, tokens, partition=0, q_dtype=F32,
               gate_dtype=F32, out_dtype=F32, cache_positions=None, stream=None) -> None:
     """Causal GQA attention with the output gate (dih_attention; p_fused_attention,
-    gpu_prefill.mm:552-570). keys/values: bf16 cache tensors [cache_positions, 512]."""
+    gpu_prefill.mm:552-570). keys/values: bf16 cache tensors [cache_positions, 512].
+    partition: the rounding partition (0: the reference's 1024; 32: every 32-key block its
+    own partition, the fastest decode form)."""
     if cache_positions is None:
         cache_positions = keys.shape[0]
     err = _errbuf()
@@ -642,7 +644,7 @@ def delta_rule(dev, state, history, conv, decay, beta, raw, out, tokens, path=0,
 
 
 def attention_partition(position, tokens, partition=0) -> int:
-    """Keys per partition dih_attention uses for these arguments."""
+    """Rounding partition dih_attention uses for these arguments (1024 unless given)."""
     n = load().dih_attention_partition(position, tokens, partition)
     if n < 0:
         raise ArgumentError("Invalid attention arguments")

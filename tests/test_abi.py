@@ -40,6 +40,15 @@ def test_only_declared_symbols_are_exported():
     assert ours == declared()
 
 
+def test_attention_default_rounding_partition_is_the_reference_one():
+    """gpu_prefill.mm:393 (attentionPartitionTokens = 1024) for every call shape; an explicit
+    partition is kept; invalid arguments give -1 (no device needed)."""
+    for position, tokens in [(0, 1), (5000, 1), (40000, 1), (0, 2048), (30720, 2048), (100, 7)]:
+        assert dh.attention_partition(position, tokens) == 1024
+    assert dh.attention_partition(100, 7, 32) == 32
+    assert dh.load().dih_attention_partition(0, 1, 48) == -1
+
+
 def test_version_string():
     assert "gfx950" in dh.version()
 

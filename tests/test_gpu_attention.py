@@ -77,15 +77,90 @@ def test_attention_random_oracle(device, inputs, base, count, offset):
     assert np.all(np.isnan(got[:offset])) and np.all(np.isnan(got[offset + count:]))
 
 
-@pytest.mark.parametrize("partition", [32, 256, 1024, 8192])
-def test_attention_partitions(device, inputs, partition):
-    """Explicit partitions, split and unsplit, through the combine kernel."""
+@pytest.mark.parametrize("count", [1, 5, 100])
+@pytest.mark.parametrize("partition", [32, 128, 256, 1024, 2048, 4096, 8192])
+def test_attention_partitions(device, inputs, partition, count):
+    """Explicit rounding partitions (gpu_prefill.mm:486-489 allows 1024..32768; any multiple
+    of 32 here): one decode token (the decode kernel's own rounding at 32, the scores pass
+    up to 4096, the general kernel above), short and multi-tile chunks."""
     I = inputs
-    position, count = 1500, 100
+    position = 5000 - count
     out = torch.zeros((count, 4096), device="cuda")
     dh.attention(device, I.dq, I.dk, I.dv, I.draw, out, position, count, partition=partition)
     torch.cuda.synchronize()
     want = orc.attention_f64(I.q[:count], I.k, I.v, I.raw[:count], position, partition=partition)
+    _check(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("position,count,partition", [(9000, 64, 0), (20000, 1, 0), (6000, 16, 0), (4000, 1, 2048),
+                                                      (3000, 100, 128), (3000, 100, 32)])
+def test_attention_rounding_points(device, position, count, partition):
+    """Inputs on which the rounding points show: queries scaled so that a few keys dominate
+    each row and values around 1 (outputs O(1)). Moving where probabilities are rounded
+    (another partition) moves 40-77 % of the outputs, a relative L2 change of 3.3e-5 to
+    1.1e-4 against the reference's double oracle; the library must stay within 1e-5 of the
+    oracle at its own partition (the default: 1024). Single outputs may differ by up to
+    1.5e-4 here: with few dominant keys, one probability whose fp32 exponential lands on
+    the other side of a bf16 rounding midpoint than the double one moves an output by
+    p * 2^-8 / sum(p), which the reference's 3e-5 bound (on its diffuse inputs) never meets.
+    (3000, 100, 128) and (3000, 100, 32) have several rounding partitions inside one
+    block's keys."""
+    n = position + count
+    (q,), s = orc.xorshift_values(0x5eed1024, count * 4096)
+    (k, v), s = orc.xorshift_values(s, n * 512, 2)
+    (r,), s = orc.xorshift_values(s, count * 8192)
+    q = (50.0 * q).reshape(count, 4096).astype(np.float32)
+    kb = orc.f32_to_bf16_bits(k).reshape(n, 512)
+    vb = orc.f32_to_bf16_bits((1.0 + v).astype(np.float32)).reshape(n, 512)
+    raw = (r * 5).reshape(count, 8192)
+    out = torch.zeros((count, 4096), device="cuda")
+    dh.attention(device, torch.from_numpy(q).cuda(), torch.from_numpy(kb.view(np.int16)).cuda(),
+                 torch.from_numpy(vb.view(np.int16)).cuda(), torch.from_numpy(raw).cuda(), out, position, count,
+                 partition=partition)
+    torch.cuda.synchronize()
+    part = dh.attention_partition(position, count, partition)
+    kf, vf = orc.bf16_bits_to_f32(kb), orc.bf16_bits_to_f32(vb)
+    want = orc.attention_f64(q, kf, vf, raw, position, partition=part)
+    got = out.cpu().numpy().astype(np.float64)
+
+    def rel(a):
+        return float(np.sqrt(np.sum((a - want) ** 2) / np.sum(want ** 2)))
+    assert np.all(np.isfinite(got))
+    assert float(np.max(np.abs(got - want))) <= 1.5e-4
+    assert rel(got) <= 1e-5, rel(got)
+    for other in {32, part // 2, 2 * part} - {part, 16}:
+        alt = orc.attention_f64(q, kf, vf, raw, position, partition=other)
+        assert rel(alt) > 3e-5, other
+
+
+@pytest.mark.parametrize("count,partition", [(100, 128), (100, 0), (1, 0)])
+def test_attention_partition_far_below_the_maximum(device, count, partition):
+    """Rounding partitions whose maximum lies about 60 (natural units; ~87 in log2) below an
+    earlier one's: KV head 0's queries all point along one vector and keys 10..13 along it
+    with scores of 60, so that for heads 0-7 every later partition's probabilities are
+    below 2^-64 of the running scale (the path that scales them down by an exact power of
+    two instead of scaling the accumulators up). Outputs must stay finite and match."""
+    position = 3000 - count
+    n = position + count
+    (q,), s = orc.xorshift_values(0x5eed60, count * 4096)
+    (k, v), s = orc.xorshift_values(s, n * 512, 2)
+    (r,), s = orc.xorshift_values(s, count * 8192)
+    q = q.reshape(count, 16, 256).astype(np.float32)   # heads 8-15: diffuse attention
+    qv = orc.round_bf16(50.0 * q[0, 0]).astype(np.float64)
+    q[:, :8] = qv.astype(np.float32)
+    q = q.reshape(count, 4096)
+    k = k.reshape(n, 512)
+    k[10:14, :256] = (qv * (60.0 * 16 / float(qv @ qv))).astype(np.float32)
+    kb = orc.f32_to_bf16_bits(k.astype(np.float32))
+    vb = orc.f32_to_bf16_bits((1.0 + v).astype(np.float32)).reshape(n, 512)
+    raw = (r * 5).reshape(count, 8192)
+    out = torch.zeros((count, 4096), device="cuda")
+    dh.attention(device, torch.from_numpy(q).cuda(), torch.from_numpy(kb.view(np.int16)).cuda(),
+                 torch.from_numpy(vb.view(np.int16)).cuda(), torch.from_numpy(raw).cuda(), out, position, count,
+                 partition=partition)
+    torch.cuda.synchronize()
+    kf, vf = orc.bf16_bits_to_f32(kb), orc.bf16_bits_to_f32(vb)
+    want = orc.attention_f64(q, kf, vf, raw, position, partition=dh.attention_partition(position, count, partition))
     _check(out.cpu().numpy(), want)
 
 
@@ -107,20 +182,21 @@ def test_attention_bf16_operands(device, inputs):
 
 @pytest.mark.parametrize("position", [0, 31, 32, 96, 127, 128, 129, 255, 1000, 8191])
 def test_attention_decode_positions(device, inputs, position):
-    """One decode token (the decode kernel: 128-key blocks of four 32-key tiles) at block
-    and tile edges, where some of a block's tiles have no keys, and with cache rows past
-    the position set to NaN (they must not be read into the result)."""
+    """One decode token (the decode kernels: 128-key blocks of four 32-key tiles, after the
+    scores pass for the default 1024-key rounding) at block and tile edges, where some of a
+    block's tiles have no keys, and with cache rows past the position set to NaN (they must
+    not be read into the result)."""
     I = inputs
     k = I.dk.clone()
     v = I.dv.clone()
     k[position + 1:] = 0x7fc0   # bf16 NaN
     v[position + 1:] = 0x7fc0
-    out = torch.full((1, 4096), float("nan"), device="cuda")
-    dh.attention(device, I.dq, k, v, I.draw, out, position, 1)
-    torch.cuda.synchronize()
-    assert dh.attention_partition(position, 1) == 32
-    want = orc.attention_f64(I.q[:1], I.k, I.v, I.raw[:1], position, partition=32)
-    _check(out.cpu().numpy(), want)
+    for partition in (0, 32):
+        out = torch.full((1, 4096), float("nan"), device="cuda")
+        dh.attention(device, I.dq, k, v, I.draw, out, position, 1, partition=partition)
+        torch.cuda.synchronize()
+        want = orc.attention_f64(I.q[:1], I.k, I.v, I.raw[:1], position, partition=partition or 1024)
+        _check(out.cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("position", [32767, 32768, 40000])
@@ -128,11 +204,12 @@ def test_attention_decode_long(device, position):
     """One decode token past 32K keys: 256, 257 and 313 block partials per head, the last
     two more than the wide combine loads in one round (its looped path)."""
     I = Inputs(1, position + 1)
-    out = torch.full((1, 4096), float("nan"), device="cuda")
-    dh.attention(device, I.dq, I.dk, I.dv, I.draw, out, position, 1)
-    torch.cuda.synchronize()
-    want = orc.attention_f64(I.q[:1], I.k, I.v, I.raw[:1], position, partition=32)
-    _check(out.cpu().numpy(), want)
+    for partition in (0, 32):
+        out = torch.full((1, 4096), float("nan"), device="cuda")
+        dh.attention(device, I.dq, I.dk, I.dv, I.draw, out, position, 1, partition=partition)
+        torch.cuda.synchronize()
+        want = orc.attention_f64(I.q[:1], I.k, I.v, I.raw[:1], position, partition=partition or 1024)
+        _check(out.cpu().numpy(), want)
 
 
 def test_attention_decode_bf16(device, inputs):
@@ -146,7 +223,7 @@ def test_attention_decode_bf16(device, inputs):
                  q_dtype=dh.BF16, gate_dtype=dh.BF16, out_dtype=dh.BF16)
     torch.cuda.synchronize()
     got = orc.bf16_bits_to_f32(out.cpu().numpy().view(np.uint16)).astype(np.float64)
-    want = orc.attention_f64(qb, I.k, I.v, rb, position, partition=32)
+    want = orc.attention_f64(qb, I.k, I.v, rb, position, partition=1024)
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + ABS_TOL)
 
 

@@ -18,7 +18,7 @@ kernel, scaled by the counters' reading for a plain copy of known size, read fro
 summaries committed under profiles/ (null when none is present).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|qmv|prefill|
-                 prefill5|dense|lm_head|copycal] [--layers L] [--cpu-seconds S] [--no-cpu]
+                 prefill5|dense|lm_head|peaks|copycal] [--layers L] [--cpu-seconds S] [--no-cpu]
 """
 import argparse
 import json
@@ -320,12 +320,14 @@ class Bench:
         """Full-attention layer (prefill_attention_bf16 + combine; p_fused_attention,
         gpu_prefill.mm:552-570): 16 query heads over 2 KV heads, head dim 256, bf16 cache.
         Cases: a 2048-token chunk on an empty cache, the last 2048-token chunk of a 32K
-        prompt, and one decode token at 32K. FLOPs count the causal work only: 1024 per
-        (query row, visible key) (q.k and p.v, 2 x 256 multiply-adds)."""
+        prompt, and one decode token at 32K, all at the reference's default 1024-key rounding
+        partition, plus the decode token with 32-key rounding (the decode kernel alone).
+        FLOPs count the causal work only: 1024 per (query row, visible key) (q.k and p.v,
+        2 x 256 multiply-adds)."""
         torch, dh = self.torch, self.dh
         out = {}
-        for name, position, T in (("chunk2048_pos0", 0, 2048), ("chunk2048_pos30720", 30720, 2048),
-                                  ("decode_pos32767", 32767, 1)):
+        for name, position, T, part in (("chunk2048_pos0", 0, 2048, 0), ("chunk2048_pos30720", 30720, 2048, 0),
+                                        ("decode_pos32767", 32767, 1, 0), ("decode_pos32767_round32", 32767, 1, 32)):
             cap = position + T
             g = torch.Generator(device="cuda").manual_seed(5)
             keys = (torch.rand((cap, 512), device="cuda", generator=g) * 0.8 - 0.4).to(torch.bfloat16)
@@ -334,17 +336,19 @@ class Bench:
             raw = torch.rand((T, 8192), device="cuda", generator=g) * 4 - 2
             y = torch.zeros((T, 4096), device="cuda")
 
-            def step(i, q=q, keys=keys, vals=vals, raw=raw, y=y, position=position, T=T):
-                dh.attention(self.dev, q, keys, vals, raw, y, position, T)
+            def step(i, q=q, keys=keys, vals=vals, raw=raw, y=y, position=position, T=T, part=part):
+                dh.attention(self.dev, q, keys, vals, raw, y, position, T, partition=part)
 
             n = max(4, steps // 12) if T > 1 else max(16, steps)
             ms, prof = self.timed_graph(step, n, min(warmup, 3))
             tot, cnt = prof.get("attention", (0, 1))
             ctot, ccnt = prof.get("attention_combine", (0, 1))
+            stot, scnt = prof.get("attention_scores", (0, 1))
             visible = T * position + T * (T + 1) // 2
             flops = 1024.0 * 16 * visible
             kv_bytes = 2 * cap * 512 * 2
-            out[name] = {"position": position, "tokens": T, "partition": dh.attention_partition(position, T),
+            out[name] = {"position": position, "tokens": T, "partition": dh.attention_partition(position, T, part),
+                         "scores_avg_us": stot / max(scnt, 1) * 1e3,
                          "ms": ms, "GFLOP": flops / 1e9, "TFLOP_s": flops / (ms * 1e-3) / 1e12,
                          "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
                          "kv_GB_s": kv_bytes / (ms * 1e-3) / 1e9, "attn_kernel_avg_us": tot / max(cnt, 1) * 1e3,
@@ -424,6 +428,67 @@ class Bench:
         torch.cuda.synchronize()
         return {"bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": steps}
 
+    def peaks(self, read_gib=4, reps=5):
+        """On-box ceilings (lib/libdih_peaks.so): a streaming read of `read_gib` GiB (well
+        above the 256 MB MALL) and a register-resident bf16 MFMA loop, each swept over a few
+        grid sizes; every point is the median of `reps` launches timed with HIP events on the
+        stream the kernels run on. The best point of each sweep is the measured ceiling."""
+        import ctypes
+        import statistics
+        torch = self.torch
+        lib = ctypes.CDLL(os.path.join(ROOT, "infer.net_amd", "lib", "libdih_peaks.so"))
+        lib.dihp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                         ctypes.c_void_p]
+        lib.dihp_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                       ctypes.c_void_p]
+        lib.dihp_mfma_loop_flops.restype = ctypes.c_double
+        lib.dihp_mfma_loop_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+        stream = torch.cuda.current_stream()
+        h = ctypes.c_void_p(stream.cuda_stream)
+
+        def timed(launch):
+            launch()
+            ms = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                launch()
+                e1.record(stream)
+                e1.synchronize()
+                ms.append(e0.elapsed_time(e1))
+            return statistics.median(ms)
+
+        nbytes = read_gib << 30
+        buf = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(0x5a5a5a5a)
+        sink = torch.empty(1 << 16, dtype=torch.int32, device="cuda")
+        read = {}
+        for blocks in (2048, 4096, 8192, 16384):
+            def launch(blocks=blocks):
+                rc = lib.dihp_stream_read(ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()),
+                                          blocks, h)
+                assert rc == 0, rc
+            read[blocks] = nbytes / (timed(launch) * 1e-3) / 1e9
+        del buf
+        ops = torch.full((64 * 8,), 0x3F80, dtype=torch.int16, device="cuda")  # bf16 1.0
+        iters = 2048
+        mfma = {}
+        for blocks in (1024, 2048, 4096):
+            out = torch.empty(blocks * lib.dihp_mfma_threads(), dtype=torch.float32, device="cuda")
+
+            def launch(blocks=blocks, out=out):
+                rc = lib.dihp_mfma_loop(ctypes.c_void_p(ops.data_ptr()), iters, ctypes.c_void_p(out.data_ptr()),
+                                        blocks, h)
+                assert rc == 0, rc
+            mfma[blocks] = lib.dihp_mfma_loop_flops(iters, blocks) / (timed(launch) * 1e-3) / 1e12
+            assert bool((out == 1024.0 * iters).all()), "MFMA probe returned a wrong sum"
+        torch.cuda.empty_cache()
+        return {"hbm_read_GB_s": max(read.values()), "mfma_bf16_TFLOP_s": max(mfma.values()),
+                "read_sweep_GB_s": {str(k): round(v, 1) for k, v in read.items()},
+                "mfma_sweep_TFLOP_s": {str(k): round(v, 1) for k, v in mfma.items()},
+                "method": f"stream read of {read_gib} GiB (dwordx4, 4 loads in flight per lane) and "
+                          f"{iters} rounds x 4 independent v_mfma_f32_32x32x16_bf16 per wave; median of "
+                          f"{reps} launches per grid size, best grid size reported"}
+
     def load(self, reps=3):
         """Checkpoint loading (dih_checkpoint_moe_layer): one config-2 MoE layer written in the
         MLX safetensors layout to a temporary directory (so the shard files sit in the page
@@ -475,10 +540,29 @@ class Bench:
         self.torch.cuda.empty_cache()
 
 
-def cpu_baseline(seconds):
+def host_description():
+    """CPU model, the cores this process may run on, and the machine's logical CPU count."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": len(os.sched_getaffinity(0)), "logical_cpus": os.cpu_count()}
+
+
+def cpu_baseline(seconds, runs=5):
     """The reference's CPU dequant-then-matmul path (oracle/oracle.c restatement of
     MatVec.cs:40-55 + quantized.mm:384-397, composed per Qwen36Model.cs:218-262) timed for
-    config 2 on this host, single-threaded like the reference."""
+    config 2 on this host in two legs: single-threaded, as the reference runs it, and on
+    every core this process may use (rows and experts split across OpenMP threads, at most
+    16: the box's CPU share). Each leg does one warm-up step, then `runs` timed runs of the
+    same number of steps; the reported figure is the median run. `value` is the all-cores
+    leg, the stronger of the two baselines."""
+    import statistics
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
@@ -488,17 +572,35 @@ def cpu_baseline(seconds):
                      orc.random_matrix(rng, 1, I, H, 8), orc.random_matrix(rng, 1, I, H, 8),
                      orc.random_matrix(rng, 1, H, I, 8), orc.random_matrix(rng, 1, 1, H, 8))
     xs = orc.round_bf16(rng.normal(size=(16, H)).astype(np.float32))
-    orc.cpu_moe_token(L, xs[0])
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        orc.cpu_moe_token(L, xs[n % 16], threads=1)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
     b = 9 * (2 * qbytes(1, I, H, 8) + qbytes(1, H, I, 8)) + qbytes(1, E, H, 8) + qbytes(1, 1, H, 8) + 6 * H
-    return {"value": b / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{n} decode MoE steps (config 2, one 8-bit layer) in {n * dt:.1f} s, "
-                      f"{dt * 1e3:.1f} ms/step, oracle/oracle.c orc_cpu_moe_token",
-            "ms_per_step": dt * 1e3}
+    host = host_description()
+    all_threads = max(1, min(16, host["nproc"]))
+
+    def leg(threads, budget):
+        t0 = time.perf_counter()
+        orc.cpu_moe_token(L, xs[0], threads=threads)  # warm-up
+        one = max(time.perf_counter() - t0, 1e-5)
+        per_run = max(1, int(budget / runs / one))
+        per_step = []
+        n = 0
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            for _ in range(per_run):
+                orc.cpu_moe_token(L, xs[n % 16], threads=threads)
+                n += 1
+            per_step.append((time.perf_counter() - t0) / per_run)
+        dt = statistics.median(per_step)
+        return {"GB_s": b / dt / 1e9, "ms_per_step": dt * 1e3, "threads": threads, "runs": runs,
+                "steps_per_run": per_run, "run_ms_per_step": [round(t * 1e3, 3) for t in per_step]}
+
+    single = leg(1, 0.6 * seconds)
+    multi = leg(all_threads, 0.4 * seconds) if all_threads > 1 else single
+    return {"value": multi["GB_s"], "unit": "GB/s", "cores": all_threads, "kind": "port",
+            "sample": f"decode MoE steps (config 2, one 8-bit layer): 1 warm-up + median of {runs} runs "
+                      f"of {multi['steps_per_run']} steps on {all_threads} threads "
+                      f"({multi['ms_per_step']:.2f} ms/step); single-thread leg {single['GB_s']:.2f} GB/s "
+                      f"over {runs} runs of {single['steps_per_run']} steps; oracle/oracle.c orc_cpu_moe_token",
+            "ms_per_step": multi["ms_per_step"], "all_cores": multi, "single_thread": single, "host": host}
 
 
 def main():
@@ -562,6 +664,10 @@ def main():
     if on("lm_head"):
         res["lm_head"] = b.lm_head(steps, warmup)
         log(f"[lm_head] {res['lm_head']['GB_s']:.0f} GB/s")
+    if on("peaks"):
+        res["peaks"] = b.peaks()
+        log(f"[peaks] HBM read {res['peaks']['hbm_read_GB_s']:.0f} GB/s, "
+            f"bf16 MFMA {res['peaks']['mfma_bf16_TFLOP_s']:.0f} TFLOP/s")
 
     if "decode" in res:
         d = res["decode"]
@@ -578,6 +684,9 @@ def main():
                     "unit": "GB/s", "frac": dom[1]["GB_s"] / PEAK_HBM_GBS if dom[1]["GB_s"] else None,
                     "traffic": traffic_from_profiles(dom[0]), "avg_us": dom[1]["avg_us"],
                     "bytes_per_launch": dom[1]["bytes"]}
+            if "peaks" in res and dom[1]["GB_s"]:
+                roof["measured_peak"] = res["peaks"]["hbm_read_GB_s"]
+                roof["frac_of_measured_peak"] = dom[1]["GB_s"] / res["peaks"]["hbm_read_GB_s"]
     else:
         k, v = next(iter(res.items()))
         if k == "attention":
@@ -601,7 +710,8 @@ def main():
             "steps": steps, "warmup": warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": head["dtype"], "data": "synthetic",
             "config": head["config"], "roofline": roof, "cpu_baseline": cpu, "tok_s": tok,
-            "secondary": {k: v for k, v in res.items() if k != "decode"}}
+            "peaks_measured": res.get("peaks"),
+            "secondary": {k: v for k, v in res.items() if k not in ("decode", "peaks")}}
     if "decode" in res:
         line["secondary"]["decode_stages"] = res["decode"]["stages"]
     print(json.dumps(line), flush=True)

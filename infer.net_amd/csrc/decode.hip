@@ -136,8 +136,9 @@ DIH_DEV float lane_x(float (&x)[32], const void *base, int x_bf16, const LaneGeo
 }
 
 // Activations staged for the 8-bit f16 dot (chunk_dot_h8). Chunk c (32 columns) is stored
-// as f16 values x * 2^-k_c, with k_c = 0 unless the chunk's largest |x| reaches 2^15 (then
-// the scaled values stay below 2^15; a power-of-two scale is exact), as four 16-byte pieces
+// as f16 values x * 2^-k_c, with k_c chosen so that the chunk's largest |x| lands in
+// [2^14, 2^15) (a power-of-two scale is exact, and every bf16 value within 2^29 of the
+// largest stays a normal, exact f16; small chunks are scaled up), as four 16-byte pieces
 // rotated by c/2 so that eight lanes reading eight chunks hit distinct bank groups. Per
 // chunk: the f32 sum of the stored f16 values (so that the 1024 offset cancels against
 // exactly the values the dot used) and 2^k_c.
@@ -160,7 +161,7 @@ DIH_DEV void stage_xh_store(const uint4 v, int H, uint32_t *xh, float *xhs, floa
         m = fmaxf(m, dppf<DIH_DPP_XOR1>(m));
         m = fmaxf(m, dppf<DIH_DPP_XOR2>(m));
         const int e = (int)((__float_as_uint(m) >> 23) & 255u) - 126;
-        const int k = e > 15 ? e - 15 : 0;
+        const int k = max(e - 15, -100);   // (an all-zero chunk: any scale)
         uint32_t p[4];
         float sum = 0.f;
 #pragma unroll

@@ -10,9 +10,11 @@
 //
 // Activations: each block stages its slot's x once in LDS (loads issued before the weight
 // ring, so waiting for them does not wait for weights). With 8-bit codes and bf16 x the
-// copy is f16 (exact for bf16 values below 2^15; a chunk reaching 2^15 is scaled by a
-// power of two) and the dot takes two codes per instruction (chunk_dot_h8); otherwise it
-// is f32. Each chunk also stores the sum of its staged values.
+// copy is f16: each 32-column chunk is scaled by a power of two that puts its largest
+// magnitude in [2^14, 2^15), which is exact and keeps every bf16 value within 2^29 of the
+// chunk's largest a normal (exact) f16. The dot takes two codes per instruction
+// (chunk_dot_h8); otherwise it is f32. Each chunk also stores the sum of its staged values
+// and its scale.
 //
 // Latency hiding: each wave keeps D row groups in flight in a register ring. The raw
 // words of a row group (codes and the bf16 bit patterns of its scales and biases) stay
@@ -111,7 +113,7 @@ DIH_DEV void xstage_store(const XStage<CPL> &X, const QmvSeg &S, uint32_t *lds) 
             m = fmaxf(m, dppf<DIH_DPP_XOR1>(m));
             m = fmaxf(m, dppf<DIH_DPP_XOR2>(m));
             const int ex = (int)((__float_as_uint(m) >> 23) & 255u) - 126;
-            const int sc = ex > 15 ? ex - 15 : 0;
+            const int sc = max(ex - 15, -100);   // (an all-zero chunk: any scale)
             uint32_t pk[4];
             sum = 0.f;
 #pragma unroll

@@ -80,6 +80,42 @@ def test_qmv_bf16_matches_fp64_oracle(device, bits, rows, columns):
         m.dispose()
 
 
+def _dynamic_range_x(rng, n, profile):
+    """bf16 activations for the f16 staging checks: 'span' gives every element a random
+    binade in 2^-20..2^15, so every 32-column chunk spans the whole range; 'tiny' is
+    N(0,1)*2^-20 (f16 subnormals unless the chunk is scaled up); 'huge' is N(0,1)*2^30."""
+    if profile == "span":
+        x = rng.choice([-1.0, 1.0], size=n) * np.exp2(rng.uniform(-20, 15, size=n))
+    elif profile == "tiny":
+        x = rng.normal(size=n) * 2.0 ** -20
+    else:
+        x = rng.normal(size=n) * 2.0 ** 30
+    return orc.f32_to_bf16_bits(x.astype(np.float32))
+
+
+@pytest.mark.parametrize("profile", ["span", "tiny", "huge"])
+def test_qmv_f16_staging_dynamic_range(device, profile):
+    """The 8-bit decode GEMV stages bf16 x as f16, each 32-column chunk scaled by the power
+    of two that puts its largest magnitude in [2^14, 2^15). That is exact for every value
+    within 2^29 of the chunk's largest, so the result stays at fp32-accumulation accuracy
+    whatever the activations' scale (config-1 shape)."""
+    rng = np.random.default_rng(11)
+    host = orc.random_matrix(rng, 1, 4096, 2048, 8)
+    m = upload(device, host)
+    try:
+        xb = _dynamic_range_x(rng, 2048, profile)
+        y = torch.zeros(4096, dtype=torch.float32, device="cuda")
+        dh.qmv(device, m, dev_bf16(xb), y, y_dtype=dh.F32)
+        torch.cuda.synchronize()
+        want = orc.qmv_f64(host, orc.bf16_bits_to_f32(xb))
+        got = y.cpu().numpy()
+        assert np.all(np.isfinite(got))
+        err = orc.rel_err(got, want)
+        assert err < 1e-5, err
+    finally:
+        m.dispose()
+
+
 def test_qmv_experts_batched_and_bad_ids(device):
     rng = np.random.default_rng(1)
     host = orc.random_matrix(rng, 9, 129, 512, 8)
@@ -308,6 +344,41 @@ def test_moe_decode_step_matches_oracle(device, bits):
             # residual = bf16(residual + y)
             assert_rounded(host_bf16(res), orc.bf16_bits_to_f32(rb) + y[0], rms(y))
             assert int(status.item()) == 0
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
+@pytest.mark.parametrize("profile", ["span", "tiny", "huge"])
+def test_moe_decode_f16_staging_dynamic_range(device, profile):
+    """The decode step's router and expert gate/up stage x as f16 per 32-column chunk (with
+    a power-of-two scale per chunk): logits, routing and outputs keep their accuracy for
+    activations spread over 2^-20..2^15 in every chunk, or entirely near 2^-20 or 2^30."""
+    rng = np.random.default_rng(12)
+    E, H, I = 256, 2048, 512
+    L = _moe_layer(rng, E, H, I, 8)
+    q, layer = _upload_layer(device, L)
+    try:
+        xb = _dynamic_range_x(rng, H, profile)
+        res = dev_bf16(np.zeros(H, dtype=np.uint16))
+        lg = torch.zeros(E, dtype=torch.float32, device="cuda")
+        ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+        probs = torch.zeros(8, dtype=torch.float32, device="cuda")
+        rout = torch.zeros((9, H), dtype=torch.float32, device="cuda")
+        dh.moe_decode(device, layer, dev_bf16(xb), res,
+                      trace=dh.make_trace(logits=lg, ids=ids, probs=probs, expert_out=rout))
+        torch.cuda.synchronize()
+        xf = orc.bf16_bits_to_f32(xb)
+        got_lg = lg.cpu().numpy()
+        assert orc.rel_err(got_lg, orc.qmv_f64(L.router, xf)) < 1e-5
+        oid, opr = orc.top8(got_lg)
+        assert np.array_equal(ids.cpu().numpy(), oid)
+        _, ro = orc.moe_f64(L, xf[None, :], oid[None, :], opr[None, :], bf16_operands=False, route_out=True)
+        got = rout.cpu().numpy()
+        assert np.all(np.isfinite(got))
+        err = orc.rel_err(got, ro)
+        assert err < 1e-4, err
     finally:
         for m in q:
             if m is not None:

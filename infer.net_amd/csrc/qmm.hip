@@ -360,6 +360,9 @@ constexpr int qmm_lds_occupancy() {
 // every step), which otherwise costs as much LDS bandwidth as the MFMAs take time.
 template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1>
 __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
+    // 32-route tiles (NT = 1) gave wrong results in the 8-bit grouped down projection, cause
+    // not found (the copy and operand index arithmetic checks out on the host): not built
+    static_assert(NT >= 2, "route tiles of 64 or more routes only");
     static_assert(!SPLIT || GATED, "only the gated kernel splits its matrices over waves");
     static_assert(RS == 1 || (!GATED && !SPLIT), "two slabs a wave: non-gated only");
     constexpr int TR = 128 * RS;             // rows per row tile

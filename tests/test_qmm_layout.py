@@ -1,0 +1,151 @@
+"""Host-side check of qmm_lds_kernel's LDS layout (infer.net_amd/csrc/qmm.hip), CPU only.
+
+The kernel's direct global->LDS copies (global_load_lds: lane L of a copy writes its 16 or 4
+bytes at the wave-uniform LDS address + L * size) and its MFMA operand reads are restated
+here from the kernel's index expressions, for every tile shape the template can take
+(8/5-bit, 1/2/4 route tiles of 32, four or eight waves, one or two 32-row slabs). The test
+then checks what the kernel relies on:
+* the copies of one step land inside their stage and never overlap;
+* every operand byte a lane reads was written by that step's copies;
+* and it is the byte the MFMA needs: weight row `wr`, codes 32h + 8j .. +7 of the K step
+  for MFMA j in lane half h, and route slot n's activations 32h + 8j .. +7 likewise;
+* the epilogue's accumulator layout covers each (row, route slot) of the tile exactly once.
+NT = 1 (32-route tiles, not built: `static_assert(NT >= 2)`) is checked as well; its index
+arithmetic is as consistent as the built widths'.
+"""
+import itertools
+
+import pytest
+
+
+def stage_layout(bits, nt, mode, rs):
+    """mode: 'down' (one matrix, four waves), 'gated' (gate and up, four waves, each wave
+    both), 'split' (gate and up, eight waves, waves 4-7 the up matrix)."""
+    split = mode == "split"
+    nw = 8 if split else 4
+    tr = 128 * rs
+    ab = 64 * bits // 8
+    a_st = tr * ab
+    nmat = 1 if mode == "down" else 2
+    wmat = 2 if mode == "gated" else 1
+    bn = 32 * nt
+    st = nmat * a_st + bn * 128
+    aq = (2 if bits == 8 else 5) * rs
+    nbw = 4 * nt // nw
+    return dict(nw=nw, tr=tr, ab=ab, a_st=a_st, nmat=nmat, wmat=wmat, bn=bn, st=st, aq=aq, nbw=nbw, split=split)
+
+
+def copies(bits, nt, mode, rs):
+    """LDS byte -> what it holds after one step's copies: ('w', matrix, row, byte) or
+    ('x', route slot, element)."""
+    L = stage_layout(bits, nt, mode, rs)
+    split = L["split"]
+    lds = {}
+
+    def put(addr, val):
+        assert 0 <= addr < L["st"], (addr, L["st"])
+        assert addr not in lds, ("two copies write one LDS byte", addr)
+        lds[addr] = val
+
+    for wave in range(L["nw"]):
+        slab = wave & 3
+        mw = wave >> 2 if split else 0
+        for mm in range(L["wmat"]):
+            m = mm + mw
+            for q in range(L["aq"]):
+                for lane in range(64):
+                    if bits == 8:
+                        rl, sl = 16 * q + (lane >> 2), lane & 3
+                        crow = slab * 32 * rs + rl
+                        coff = 16 * (sl ^ ((rl >> 2) & 3))
+                        dst = m * L["a_st"] + (slab * 32 * rs + 16 * q) * 64 + 16 * lane
+                        for b in range(16):
+                            put(dst + b, ("w", m, crow, coff + b))
+                    else:
+                        i = 64 * q + lane
+                        rl = i // 10
+                        crow = slab * 32 * rs + rl
+                        coff = 4 * (i - rl * 10)
+                        dst = m * L["a_st"] + slab * 32 * rs * 40 + q * 256 + 4 * lane
+                        for b in range(4):
+                            put(dst + b, ("w", m, crow, coff + b))
+        for i in range(L["nbw"]):
+            for lane in range(64):
+                n = (L["nw"] * i + wave) * 8 + (lane >> 3)
+                sl = lane & 7
+                src_el = 8 * (sl ^ ((n >> 1) & 7))
+                dst = L["nmat"] * L["a_st"] + (L["nw"] * i + wave) * 8 * 128 + 16 * lane
+                for b in range(16):
+                    put(dst + b, ("x", n, src_el + b // 2, b % 2))
+    return L, lds
+
+
+SHAPES = [(bits, nt, mode, rs) for bits, nt, mode, rs in itertools.product((8, 5), (1, 2, 4), ("down", "gated", "split"), (1, 2))
+          if (mode == "down" or rs == 1) and (4 * nt) % (8 if mode == "split" else 4) == 0]
+
+
+@pytest.mark.parametrize("bits,nt,mode,rs", SHAPES)
+def test_operand_reads_see_their_copies(bits, nt, mode, rs):
+    L, lds = copies(bits, nt, mode, rs)
+    nw, split = L["nw"], L["split"]
+    for wave in range(nw):
+        slab = wave & 3
+        mw = wave >> 2 if split else 0
+        for lane in range(64):
+            r, h = lane & 31, lane >> 5
+            # weights: the lane's chunk (codes 32h..32h+31 of row wr in this K step)
+            for rsi, mm in itertools.product(range(rs), range(L["wmat"])):
+                wr = slab * 32 * rs + 32 * rsi + r
+                m = mm + mw
+                if bits == 8:
+                    sw = (r >> 2) & 3
+                    ra = m * L["a_st"] + wr * 64
+                    got = [lds[ra + 16 * ((2 * h) ^ sw) + b] for b in range(16)] + \
+                          [lds[ra + 16 * ((2 * h + 1) ^ sw) + b] for b in range(16)]
+                    want = [("w", m, wr, 32 * h + b) for b in range(32)]
+                else:
+                    ra = m * L["a_st"] + (wr * 10 + 5 * h) * 4
+                    got = [lds[ra + b] for b in range(20)]
+                    want = [("w", m, wr, 20 * h + b) for b in range(20)]
+                assert got == want, (wave, lane, rsi, m)
+            # activations: MFMA j reads route slot n's elements 32h + 8j .. +7
+            bb = L["nmat"] * L["a_st"]
+            for j in range(4):
+                for i in range(nt):
+                    n = 32 * i + r
+                    pc = 4 * h + j
+                    addr = bb + n * 128 + 16 * (pc ^ ((n >> 1) & 7))
+                    got = [lds[addr + b] for b in range(16)]
+                    want = [("x", n, 32 * h + 8 * j + b // 2, b % 2) for b in range(16)]
+                    assert got == want, (wave, lane, j, i)
+
+
+@pytest.mark.parametrize("bits,nt,mode,rs", SHAPES)
+def test_copies_fill_the_stage(bits, nt, mode, rs):
+    """Each step's copies write every byte of the weight rows and route slots once."""
+    L, lds = copies(bits, nt, mode, rs)
+    weights = sorted(v for v in lds.values() if v[0] == "w")
+    want_w = sorted(("w", m, row, b) for m in range(L["nmat"]) for row in range(L["tr"]) for b in range(L["ab"]))
+    assert weights == want_w
+    acts = sorted(v for v in lds.values() if v[0] == "x")
+    want_x = sorted(("x", n, e, half) for n in range(L["bn"]) for e in range(64) for half in range(2))
+    assert acts == want_x
+
+
+@pytest.mark.parametrize("nt", [1, 2, 4])
+def test_epilogue_covers_each_output_once(nt):
+    """Accumulator element k of lane (r, h) in route tile i of slab `slab` is output row
+    slab*32 + 8*(k/4) + 4h + k%4 of the tile and route slot 32i + r (the 32x32x16 MFMA's
+    C layout), as the epilogue stores it."""
+    seen = {}
+    for slab in range(4):
+        for lane in range(64):
+            r, h = lane & 31, lane >> 5
+            for i in range(nt):
+                for q in range(4):
+                    for k in range(4):
+                        row = slab * 32 + 8 * q + 4 * h + k
+                        key = (row, 32 * i + r)
+                        assert key not in seen
+                        seen[key] = True
+    assert len(seen) == 128 * 32 * nt

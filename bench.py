@@ -443,6 +443,9 @@ class Bench:
                                        ctypes.c_void_p]
         lib.dihp_mfma_loop_flops.restype = ctypes.c_double
         lib.dihp_mfma_loop_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+        lib.dihp_stream_read_pieces.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+        lib.dihp_stream_read_pieces_blocks.restype = ctypes.c_size_t
+        lib.dihp_stream_read_pieces_blocks.argtypes = [ctypes.c_size_t]
         stream = torch.cuda.current_stream()
         h = ctypes.c_void_p(stream.cuda_stream)
 
@@ -468,7 +471,14 @@ class Bench:
                                           blocks, h)
                 assert rc == 0, rc
             read[blocks] = nbytes / (timed(launch) * 1e-3) / 1e9
-        del buf
+        nb = int(lib.dihp_stream_read_pieces_blocks(nbytes))
+        sink2 = torch.empty(nb, dtype=torch.int32, device="cuda")
+
+        def launch_pieces():
+            rc = lib.dihp_stream_read_pieces(ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(sink2.data_ptr()), h)
+            assert rc == 0, rc
+        read["pieces"] = nbytes / (timed(launch_pieces) * 1e-3) / 1e9
+        del buf, sink2
         ops = torch.full((64 * 8,), 0x3F80, dtype=torch.int16, device="cuda")  # bf16 1.0
         iters = 2048
         mfma = {}
@@ -485,7 +495,8 @@ class Bench:
         return {"hbm_read_GB_s": max(read.values()), "mfma_bf16_TFLOP_s": max(mfma.values()),
                 "read_sweep_GB_s": {str(k): round(v, 1) for k, v in read.items()},
                 "mfma_sweep_TFLOP_s": {str(k): round(v, 1) for k, v in mfma.items()},
-                "method": f"stream read of {read_gib} GiB (dwordx4, 4 loads in flight per lane) and "
+                "method": f"stream read of {read_gib} GiB (grid-stride dwordx4 with 4 loads in flight per lane over "
+                          f"2K-16K blocks, and one-shot 32 KB blocks of non-temporal loads, 8 in flight per lane) and "
                           f"{iters} rounds x 4 independent v_mfma_f32_32x32x16_bf16 per wave; median of "
                           f"{reps} launches per grid size, best grid size reported"}
 

@@ -23,6 +23,12 @@ extern "C" {
  * XOR over sink[0..blocks) equals the XOR of every word of the buffer. */
 int dihp_stream_read(const void *buffer, size_t bytes, uint32_t *sink, int blocks, hipStream_t stream);
 
+/* The same read as one-shot blocks: block b XORs the 32 KB piece at buffer + b * 32 KB
+ * (non-temporal loads, eight 16-byte loads a thread in flight at once) into sink[b]; the
+ * grid is dihp_stream_read_pieces_blocks(bytes) blocks. */
+int dihp_stream_read_pieces(const void *buffer, size_t bytes, uint32_t *sink, hipStream_t stream);
+size_t dihp_stream_read_pieces_blocks(size_t bytes);
+
 /* `blocks` blocks of dihp_mfma_threads() threads; every wave issues `iters` rounds of four
  * independent v_mfma_f32_32x32x16_bf16 with A = B = operands[lane*8 .. lane*8+8) (bf16 bits,
  * 64 lanes x 8). out[block*threads + t] receives the sum of lane t's accumulators; with every

@@ -48,6 +48,36 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4 *
     }
 }
 
+// One-shot form: block b XORs the 32 KB at p + b * 32 KB (each thread eight 16-byte
+// non-temporal loads, all in flight before the first is used), so the grid is
+// bytes / 32 KB blocks that each read one contiguous piece and exit.
+constexpr int kPieceLoads = 8;
+constexpr size_t kPieceBytes = (size_t)kReadThreads * kPieceLoads * 16;
+
+__global__ __launch_bounds__(kReadThreads) void stream_read_pieces_kernel(const uint4 *__restrict__ p, size_t n16,
+                                                                          uint32_t *__restrict__ sink) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const size_t base = (size_t)blockIdx.x * (kPieceBytes / 16) + threadIdx.x;
+    u32x4 v[kPieceLoads];
+#pragma unroll
+    for (int u = 0; u < kPieceLoads; u++) {
+        const size_t k = base + (size_t)u * kReadThreads;
+        v[u] = k < n16 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p + k)) : u32x4{0, 0, 0, 0};
+    }
+    uint32_t r = 0;
+#pragma unroll
+    for (int u = 0; u < kPieceLoads; u++) r ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int o = 32; o > 0; o >>= 1) r ^= __shfl_xor(r, o, 64);
+    __shared__ uint32_t part[kReadThreads / 64];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t s = 0;
+        for (int w = 0; w < kReadThreads / 64; ++w) s ^= part[w];
+        sink[blockIdx.x] = s;
+    }
+}
+
 constexpr int kMfmaThreads = 256;
 constexpr int kChains = 4;
 
@@ -84,6 +114,18 @@ int dihp_stream_read(const void *buffer, size_t bytes, uint32_t *sink, int block
                        static_cast<const uint4 *>(buffer), bytes / 16, sink);
     return int(hipGetLastError());
 }
+
+int dihp_stream_read_pieces(const void *buffer, size_t bytes, uint32_t *sink, hipStream_t stream) {
+    if (!buffer || !sink || bytes == 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(buffer) % 16 != 0)
+        return int(hipErrorInvalidValue);
+    const size_t blocks = (bytes + kPieceBytes - 1) / kPieceBytes;
+    if (blocks > 0x7fffffffu) return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL(stream_read_pieces_kernel, dim3((unsigned)blocks), dim3(kReadThreads), 0, stream,
+                       static_cast<const uint4 *>(buffer), bytes / 16, sink);
+    return int(hipGetLastError());
+}
+
+size_t dihp_stream_read_pieces_blocks(size_t bytes) { return (bytes + kPieceBytes - 1) / kPieceBytes; }
 
 int dihp_mfma_loop(const short *operands, int iters, float *out, int blocks, hipStream_t stream) {
     if (!operands || !out || blocks <= 0 || iters <= 0) return int(hipErrorInvalidValue);

@@ -19,19 +19,23 @@ def load():
     lib.dihp_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     lib.dihp_mfma_loop_flops.restype = ctypes.c_double
     lib.dihp_mfma_loop_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.dihp_stream_read_pieces.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    lib.dihp_stream_read_pieces_blocks.restype = ctypes.c_size_t
+    lib.dihp_stream_read_pieces_blocks.argtypes = [ctypes.c_size_t]
     return lib
 
 
 def test_probe_library_exports_its_header():
     text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
     names = sorted(set(re.findall(r"\b(dihp_[a-z0-9_]+)\s*\(", text)))
-    assert len(names) == 4
+    assert len(names) == 6
     lib = load()
     for n in names:
         assert hasattr(lib, n), n
     # 2*32*32*16 flops per MFMA, 4 waves per 256-thread block, 4 chains
     assert lib.dihp_mfma_loop_flops(10, 3) == 3 * 4 * 4 * 10 * 32768.0
     assert lib.dihp_mfma_threads() == 256
+    assert lib.dihp_stream_read_pieces_blocks(32768) == 1 and lib.dihp_stream_read_pieces_blocks(32784) == 2
 
 
 def test_probe_rejects_bad_arguments_before_any_launch():
@@ -55,6 +59,13 @@ def test_stream_read_checksum(nbytes, blocks):
     torch.cuda.synchronize()
     got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
     assert got == np.bitwise_xor.reduce(host)
+    # the one-shot form (a partial last piece when nbytes is not a multiple of 32 KB)
+    nb = lib.dihp_stream_read_pieces_blocks(nbytes)
+    sink2 = torch.zeros(nb, dtype=torch.int32, device="cuda")
+    assert lib.dihp_stream_read_pieces(ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(sink2.data_ptr()),
+                                       ctypes.c_void_p(s.cuda_stream)) == 0
+    torch.cuda.synchronize()
+    assert np.bitwise_xor.reduce(sink2.cpu().numpy().view(np.uint32)) == np.bitwise_xor.reduce(host)
 
 
 @pytest.mark.gpu

@@ -384,7 +384,10 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     // lives in LDS (the split form adds the SwiGLU exchange), so that two blocks fit on a
     // CU when the stages take half of it.
     __shared__ __align__(16) unsigned char st0[ST], st1[ST], st2[ST], st3[ST];
-    __shared__ __align__(16) float xch[SPLIT ? 4 * NT * 16 * 64 : 1];
+    // split: silu(gate) of XNT route tiles at a time (in halves when four tiles would not fit
+    // beside the stages)
+    constexpr int XNT = SPLIT && NT > 2 ? NT / 2 : NT;
+    __shared__ __align__(16) float xch[SPLIT ? 4 * XNT * 16 * 64 : 1];
     lds_escape(st0, st1, st2, st3, xch);
     auto stage_base = [&](int stage) -> unsigned char * {
         return stage == 0 ? st0 : stage == 1 ? st1 : stage == 2 ? st2 : st3;
@@ -629,14 +632,21 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
 
         // ---- epilogue of row tile rt0 + ti: lane holds route n = 32i + r, rows
         // 8*(k/4) + 4h + (k%4) of the slab's 32. Split: the gate waves hand silu(g) to the up
-        // waves of the same slab through LDS (identical lane layouts); the up waves store.
+        // waves of the same slab through LDS (identical lane layouts), XNT route tiles at a
+        // time; the up waves store.
+#pragma unroll
+        for (int half = 0; half < NT / XNT; half++) {
         if constexpr (SPLIT) {
-            float *xw = xch + slab * NT * 16 * 64 + lane;
+            if (half > 0) {   // the up waves have read the previous half
+                wait_lgkm0();
+                barrier_no_fence();
+            }
+            float *xw = xch + slab * XNT * 16 * 64 + lane;
             if (mw == 0) {
 #pragma unroll
-                for (int i = 0; i < NT; i++) {
+                for (int i = 0; i < XNT; i++) {
 #pragma unroll
-                    for (int k = 0; k < 16; k++) xw[(i * 16 + k) * 64] = siluf_(acc0[0][i][k]);
+                    for (int k = 0; k < 16; k++) xw[(i * 16 + k) * 64] = siluf_(acc0[0][half * XNT + i][k]);
                 }
             }
             wait_lgkm0();
@@ -646,7 +656,8 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
         for (int rs = 0; rs < RS; rs++) {
         const int row_base = (rt0 + ti) * TR + slab * 32 * RS + 32 * rs;
 #pragma unroll
-        for (int i = 0; i < NT; i++) {
+        for (int ii = 0; ii < XNT; ii++) {
+            const int i = half * XNT + ii;
             const int n = 32 * i + r;
             if (n >= nvalid || (SPLIT && mw == 0)) continue;
             const int route = out_route[i];
@@ -657,7 +668,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const float g = acc0[rs][i][4 * q + k];
-                    if constexpr (SPLIT) v[k] = xch[(slab * NT * 16 + i * 16 + 4 * q + k) * 64 + lane] * g;
+                    if constexpr (SPLIT) v[k] = xch[(slab * XNT * 16 + ii * 16 + 4 * q + k) * 64 + lane] * g;
                     else if constexpr (GATED) v[k] = siluf_(g) * acc1[i][4 * q + k];
                     else v[k] = g;
                 }
@@ -681,6 +692,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
                     }
                 }
             }
+        }
         }
         }
         zero_acc();
@@ -731,7 +743,15 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     // routes, and the narrower tile lets two blocks share a CU.
     const bool gated = m1 != nullptr;
     const bool streaming = m0->columns % 512 == 0;
-    const int nt = streaming && !a.dense && !gated ? 2 : (gated ? 2 : 4);
+    // 5-bit gated (the split eight-wave form) takes 128-route tiles when experts average
+    // more than 48 routes (uniform routing over E experts: 8T/E): 64-route tiles would give
+    // an expert of 65-127 routes a second, mostly empty chunk and dequantize its weights
+    // twice (config 4: 64 routes on average, at most ~90)
+    const bool wide_gated = streaming && gated && !a.dense && m0->bits == 5 &&
+                            (size_t)a.tokens * 8 > (size_t)48 * (size_t)std::max(1, m0->experts);
+    // (the grouped down projection keeps 64-route tiles: 96-route tiles, still two blocks a
+    // CU, measured 195 -> 209 us on config 4, and 128-route tiles 211 -> 274 us)
+    const int nt = streaming && !a.dense && !gated ? 2 : (gated ? (wide_gated ? 4 : 2) : 4);
     const int bn = 32 * nt;
     // dense streaming GEMMs with enough (256-row tile, route chunk) items to fill the GPU:
     // two 32-row slabs per wave (256-row tiles)
@@ -773,6 +793,7 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         }
         DIH_QMM_LDS_CASE(8, true, 2, false) DIH_QMM_LDS_CASE(8, false, 2, false) DIH_QMM_LDS_CASE(8, false, 4, false)
         DIH_QMM_LDS_CASE(5, true, 2, false) DIH_QMM_LDS_CASE(5, false, 2, false) DIH_QMM_LDS_CASE(5, false, 4, false)
+        DIH_QMM_LDS_CASE(5, true, 4, false)
         DIH_QMM_LDS_CASE(8, false, 4, true) DIH_QMM_LDS_CASE(5, false, 4, true)
 #undef DIH_QMM_LDS_CASE
     }

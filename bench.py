@@ -273,12 +273,14 @@ class Bench:
                 dh.dense(self.dev, m, T, x, y, y_dtype=dh.BF16)
 
             ms, prof = self.timed_graph(step, max(2, steps // 4), min(warmup, 3))
-            tot, cnt = prof.get("dense_qmm", (0, 1))
-            kern = tot / max(cnt, 1)
+            # the fused tile ("dense_qmm"), or the dequantization pass and the bf16 GEMM
+            stage_ms = {k: tot / max(cnt, 1) for k, (tot, cnt) in prof.items() if k.startswith("dense")}
+            kern = sum(stage_ms.values())
             flops = 2.0 * T * R * C
             out[name] = {"rows": R, "cols": C, "ms": ms, "TFLOP_s": flops / (ms * 1e-3) / 1e12,
                          "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-                         "kernel_avg_us": kern * 1e3}
+                         "kernel_avg_us": kern * 1e3,
+                         "stages_us": {k: v * 1e3 for k, v in stage_ms.items()}}
             m.dispose()
             del x, y
         tot_f = sum(2.0 * T * r * c for r, c in shapes.values())

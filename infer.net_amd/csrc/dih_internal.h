@@ -58,13 +58,16 @@ struct Context {
     // address, looked up once per device), or null with the lookup's error
     void *noalloc = nullptr;
     std::string noalloc_error;
+    // hipBLASLt handle and the dense projections' GEMM plans (dense_blas.hip), created on
+    // first use
+    void *blas = nullptr;
     uint32_t magic = 0x44494358u;
 };
 
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_W16, S_BLASWS, S_COUNT_
 };
 static_assert(S_COUNT_ <= (int)(sizeof(Context::ws) / sizeof(Scratch)), "scratch table too small");
 
@@ -229,6 +232,13 @@ int attention_split(int position, int tokens, int round);
 int attention_partials(int position, int tokens, int partition);
 // Floats of score scratch the decode scores pass needs (0: none).
 size_t attention_score_floats(int position, int tokens, int round, int partition);
+
+// Dense projection of a long chunk: matrix dequantized into bf16 scratch, then a hipBLASLt
+// bf16 GEMM with f32 accumulation (dense_blas.hip). blas_release frees the context's
+// hipBLASLt state.
+bool launch_dense_blas(Context *c, const Matrix *m, int tokens, const uint16_t *x, void *y, bool y_bf16,
+                       hipStream_t s, char *error, int capacity);
+void blas_release(Context *c);
 bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity);
 
 // Gated delta rule over a chunk (delta.hip): state [32][128][128] f32 and history

@@ -492,7 +492,38 @@ def test_dense_matches_oracle(device, bits, rows, columns, T):
         m.dispose()
 
 
-@pytest.mark.parametrize("bits,rows,columns,T", [(8, 2048, 512, 4096), (5, 2000, 512, 4000)])
+@pytest.mark.parametrize("bits,rows,columns,T,y_bf16", [(8, 300, 512, 1024, False), (8, 2048, 4096, 512, True),
+                                                        (5, 1000, 2048, 1100, False), (5, 64, 256, 2048, True),
+                                                        (8, 4100, 1024, 512, False)])
+def test_dense_long_chunks_bf16_gemm(device, bits, rows, columns, T, y_bf16):
+    """Long chunks (1024 tokens and more, or 512 and more for matrices of up to 4096 rows)
+    run as one dequantization pass into bf16 and a bf16 GEMM with f32 accumulation (the
+    reference's BF16 dense path, prefill_bf16.mm:7-53): the result is the fp64 product of
+    the same bf16-rounded operands within fp32 accumulation error. (8, 4100, 1024, 512)
+    stays on the fused tile (more than 4096 rows at 512 tokens)."""
+    rng = np.random.default_rng(rows * 7 + T)
+    host = orc.random_matrix(rng, 1, rows, columns, bits)
+    m = upload(device, host)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, columns)).astype(np.float32))
+        y = torch.zeros((T, rows), dtype=torch.int16 if y_bf16 else torch.float32, device="cuda")
+        dh.dense(device, m, T, dev_bf16(xb), y, y_dtype=dh.BF16 if y_bf16 else dh.F32)
+        # a second call reuses the cached plan
+        y2 = torch.zeros_like(y)
+        dh.dense(device, m, T, dev_bf16(xb), y2, y_dtype=dh.BF16 if y_bf16 else dh.F32)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2)
+        xf = orc.bf16_bits_to_f32(xb)
+        want_bf = orc.dense_f64(host, xf, round_operands=True)
+        if y_bf16:
+            assert_rounded(host_bf16(y), want_bf, rms(want_bf) * 1e-2)
+        else:
+            assert orc.rel_err(y.cpu().numpy(), want_bf) < 1e-4
+    finally:
+        m.dispose()
+
+
+@pytest.mark.parametrize("bits,rows,columns,T", [(8, 16384, 512, 512), (5, 16400, 512, 520)])
 def test_dense_two_slab_tiles(device, bits, rows, columns, T):
     """Dense launches with at least 256 (256-row tile, 128-token chunk) items run 256-row
     tiles, two 32-row slabs a wave; ragged rows and tokens included."""

@@ -236,17 +236,21 @@ class Bench:
         stages = {}
         for name, (tot, cnt) in prof.items():
             stages[name] = {"avg_us": tot / max(cnt, 1) * 1e3}
-        gu = prof.get("prefill_gate_up", (0, 1))
-        dn = prof.get("prefill_down", (0, 1))
-        gu_ms, dn_ms = gu[0] / max(gu[1], 1), dn[0] / max(dn[1], 1)
+        def stage_ms(name):
+            tot, cnt = prof.get(name, (0, 1))
+            return tot / max(cnt, 1)
+        gu_ms = stage_ms("prefill_gate_up")
+        dn_ms = stage_ms("prefill_down")
         gu_bytes = (touched + 1) * 2 * qbytes(1, I, H, bits)
         dn_bytes = (touched + 1) * qbytes(1, H, I, bits)
         if gu_ms > 0:
-            stages["prefill_gate_up"].update(
+            stages.setdefault("prefill_gate_up", {"avg_us": 0.0})
+            stages["prefill_gate_up"].update(avg_us=gu_ms * 1e3,
                 bytes=gu_bytes, GB_s=gu_bytes / (gu_ms * 1e-3) / 1e9,
                 TFLOP_s=(2.0 / 3.0) * flops / (gu_ms * 1e-3) / 1e12)
         if dn_ms > 0:
-            stages["prefill_down"].update(
+            stages.setdefault("prefill_down", {"avg_us": 0.0})
+            stages["prefill_down"].update(avg_us=dn_ms * 1e3,
                 bytes=dn_bytes, GB_s=dn_bytes / (dn_ms * 1e-3) / 1e9,
                 TFLOP_s=(1.0 / 3.0) * flops / (dn_ms * 1e-3) / 1e12)
         self.free(built)

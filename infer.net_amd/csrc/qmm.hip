@@ -104,6 +104,33 @@ DIH_DEV int chunk_of(const uint32_t *counts, int ngroups, int ci, int &group, in
     return total;
 }
 
+// Total chunks of up to BN routes over the groups, the count chunk_of returns. One wave;
+// every lane receives it.
+template <int BN>
+DIH_DEV int chunk_total(const uint32_t *counts, int ngroups) {
+    const int lane = threadIdx.x & 63;
+    int run = 0;
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+        const int g = lane * 5 + i;
+        const int raw = g < ngroups ? (int)counts[g] : 0;
+        run += (raw + BN - 1) / BN;
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) run += __shfl_xor(run, d, 64);
+    return run;
+}
+
+// Logical work item of physical block b when `items` items run on a grid sized for an
+// upper bound of them: L = (b % 8) * per + b / 8 with per = ceil(items / 8), so that
+// consecutive items share an XCD (and its L2) and the actual items, not the bound, are
+// spread over all eight XCDs. -1 for a block with no item.
+DIH_DEV int xcd_item(int b, int items) {
+    const int per = (items + 7) >> 3;
+    const int L = (b & 7) * per + (b >> 3);
+    return (b >> 3) < per && L < items ? L : -1;
+}
+
 // The MFMAs of one 64-column K step over the first NTU route tiles; each 16-column slice's
 // B operands are read from LDS before its MFMAs so the reads overlap.
 template <bool GATED, int NTU, int NT>
@@ -136,15 +163,15 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     // ---- which work item is this block? Physical block b runs logical item
-    // L = (b % 8) * (grid / 8) + b / 8 (consecutive items on one XCD at nearly the same time),
+    // L = xcd_item(b, items) (consecutive items on one XCD at nearly the same time),
     // item L = chunk * row_tiles + row tile.
     if (wave == 0) {
         int e = 0, first = 0, nvalid = 0, rt = -1;
-        const int b = blockIdx.x, per = (int)(gridDim.x >> 3);
-        const int L = (b & 7) * per + (b >> 3);
-        const int ci = L / P.row_tiles;
+        const int chunks = P.dense ? (P.tokens + BN - 1) / BN : chunk_total<BN>(P.counts, P.ngroups);
+        const int L = xcd_item((int)blockIdx.x, chunks * P.row_tiles);
+        const int ci = L < 0 ? chunks : L / P.row_tiles;
         if (P.dense) {
-            if (ci * BN < P.tokens) {
+            if (L >= 0 && ci * BN < P.tokens) {
                 rt = L - ci * P.row_tiles;
                 first = ci * BN;
                 nvalid = min(BN, P.tokens - first);
@@ -152,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
         } else {
             int count;
             const int total = chunk_of<BN>(P.counts, P.ngroups, ci, e, first, count);
-            if (ci < total) {
+            if (L >= 0 && ci < total) {
                 rt = L - ci * P.row_tiles;
                 nvalid = min(BN, count - first);
             }
@@ -398,21 +425,21 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     const int slab = wave & 3;                // 32-row slab of the 128-row tile
     const int mw = SPLIT ? wave >> 2 : 0;     // split: the matrix this wave computes
     // ---- work item (every wave derives it): physical block b runs logical item
-    // L = (b % 8) * (grid / 8) + b / 8; L = chunk * rt_groups + row-tile group, a group
-    // being up to rtb consecutive row tiles
+    // L = xcd_item(b, items); L = chunk * rt_groups + row-tile group, a group being up to
+    // rtb consecutive row tiles
     int e = 0, first = 0, nvalid = 0, rt0 = -1, nrt = 0;
     {
-        const int b = blockIdx.x, per = (int)(gridDim.x >> 3);
-        const int L = (b & 7) * per + (b >> 3);
-        const int ci = L / P.rt_groups;
+        const int chunks = P.dense ? (P.tokens + BN - 1) / BN : chunk_total<BN>(P.counts, P.ngroups);
+        const int L = xcd_item((int)blockIdx.x, chunks * P.rt_groups);
+        const int ci = L < 0 ? chunks : L / P.rt_groups;
         bool ok;
         if (P.dense) {
-            ok = ci * BN < P.tokens;
+            ok = L >= 0 && ci * BN < P.tokens;
             if (ok) { first = ci * BN; nvalid = min(BN, P.tokens - first); }
         } else {
             int count;
             const int total = chunk_of<BN>(P.counts, P.ngroups, ci, e, first, count);
-            ok = ci < total;
+            ok = L >= 0 && ci < total;
             if (ok) nvalid = min(BN, count - first);
         }
         if (ok) {

@@ -747,11 +747,10 @@ __attribute__((visibility("default"))) int dih_moe_decode(void *ctx, const dih_m
 namespace dih {
 // Device buffers of one decode MoE step (all fully written before they are read, so none
 // needs clearing): logits [E], shared route [1], shared SwiGLU [Is], slot SwiGLU [8*I],
-// shared down [H], ids [8], probs [8], status [1], router candidates [128] float2.
+// shared down [H], ids [8], probs [8], status [1].
 struct DecodeBuffers {
     float *lg, *srt, *sact, *act, *sout, *probs;
     uint32_t *ids, *status;
-    float2 *cand;
 };
 
 // Carves the step's buffers from `base` at 256-byte boundaries; returns the bytes used.
@@ -770,7 +769,6 @@ static size_t carve_decode(unsigned char *base, int E, int H, int I, int Is, Dec
     b.ids = reinterpret_cast<uint32_t *>(take(8 * 8 * 4));
     b.probs = reinterpret_cast<float *>(take(8 * 4));
     b.status = reinterpret_cast<uint32_t *>(take(16));
-    b.cand = reinterpret_cast<float2 *>(take(128 * sizeof(float2)));
     return off;
 }
 
@@ -814,9 +812,8 @@ static int moe_decode(Context *c, const dih_moe_layer *L, const void *x, const f
         bufs.ids = static_cast<uint32_t *>(ctx_scratch(c, S_IDS, 8 * 8 * 4, error, capacity));
         bufs.probs = static_cast<float *>(ctx_scratch(c, S_PROBS, 8 * 4, error, capacity));
         bufs.status = static_cast<uint32_t *>(ctx_scratch(c, S_STATUS, 16, error, capacity));
-        bufs.cand = static_cast<float2 *>(ctx_scratch(c, S_CAND, 128 * sizeof(float2), error, capacity));
         if (!bufs.lg || !bufs.srt || !bufs.sact || !bufs.act || !bufs.sout || !bufs.ids || !bufs.probs ||
-            !bufs.status || !bufs.cand)
+            !bufs.status)
             return -1;
     }
     float *lg = bufs.lg, *srt = bufs.srt, *sact = bufs.sact, *act = bufs.act, *sout = bufs.sout;
@@ -825,13 +822,12 @@ static int moe_decode(Context *c, const dih_moe_layer *L, const void *x, const f
     hipStream_t s = pick(c, stream);
     ProfScope prof_scope(fixed ? nullptr : c);
     if (decode_fast_path_ok(router, gate, down, sg, sd, sr)) {
-        float2 *cand = bufs.cand;
         DecodeLaunch a;
         a.router = router; a.gate = gate; a.up = up; a.down = down;
         a.shared_gate = sg; a.shared_up = su; a.shared_down = sd; a.shared_route = sr;
         a.logits_in = logits;
         a.logits = trace && trace->logits ? trace->logits : lg;
-        a.cand = cand; a.sact = sact; a.sroute = srt; a.act = act;
+        a.sact = sact; a.sroute = srt; a.act = act;
         a.ids = trace && trace->ids ? trace->ids : ids;
         a.probs = trace && trace->probs ? trace->probs : probs;
         a.status = trace ? trace->status : nullptr;

@@ -2,13 +2,14 @@
 // graph_top8 gpu_graph.mm:134-146 and graph_merge_norm gpu_graph.mm:48-61; host form
 // Qwen36Model.cs:218-245):
 //
-//   K1 router/shared  : four-wave blocks spread over many CUs. Router logits in 16-expert
-//                       chunks; each chunk block ranks its 16 logits in LDS and writes its
-//                       top-8 as candidates (value, id). The same launch computes the
-//                       shared expert's gate/up SwiGLU and the shared-expert sigmoid gate row.
-//   K2 experts gate/up: every block merges the <= 128 candidates by rank (the top-8 of the
-//                       union of per-chunk top-8s is the global top-8, ties to the lowest
-//                       id) and streams one gated row group per wave of its slot's expert.
+//   K1 router/shared  : four-wave blocks spread over many CUs. Router logits four experts
+//                       a block at 2048 columns (one row a wave: a block's weights are
+//                       8.7 KB, so the router's 557 KB spread over 64 CUs). The same launch
+//                       computes the shared expert's gate/up SwiGLU and the shared-expert
+//                       sigmoid gate row.
+//   K2 experts gate/up: every block ranks the <= 256 logits (top-8 of each 32, then the 64
+//                       kept; ties to the lowest id) and streams one gated row group per
+//                       wave of its slot's expert.
 //   K3 down + merge   : blocks of nine waves; waves 0..7 compute the selected experts'
 //                       down rows for the block's output rows, wave 8 the shared expert's;
 //                       the merge y = sigmoid(route)*shared + sum_slot p_slot*expert_slot
@@ -25,11 +26,10 @@ namespace dih {
 
 namespace {
 
-constexpr int kChunkExperts = 16;  // experts per router block (a block's top-8 are candidates)
 constexpr int kK1Waves = 4;        // waves per K1 block: the launch spreads over many CUs
-constexpr int kWaves = 16;         // waves per K2 block (at least 2: 128 candidate threads)
-constexpr int kRouterGroups = 4;   // K1 router: row groups per wave (16 rows per block)
-constexpr int kMaxCand = 128;      // candidates: 8 per chunk, at most 256 experts
+constexpr int kWaves = 16;         // waves per K2 block
+constexpr int kRouterGroups = 1;   // K1 router: row groups per wave
+constexpr int kMaxExperts = 256;   // routed experts: K2 ranks them with four lanes each
 constexpr int kDownGroups = 2;     // K3: row groups per wave
 
 // One lane's share of NG row groups of one matrix.
@@ -206,20 +206,28 @@ DIH_DEV void rows_dot_h8(const Rows<8, NG> &R, const uint32_t (&xr)[16], float x
     }
 }
 
-// Sort key of a candidate: larger key = earlier in (value desc, id asc) order, with -0
-// equal to +0 (finite values; a non-finite router logit makes the step fail anyway).
-DIH_DEV unsigned long long rank_key(float v, uint32_t id) {
+// Order-preserving key of a router logit: larger key = larger value, -0 equal to +0. Finite
+// values map to keys >= 0x00800000, so key 0 can stand for "no expert".
+DIH_DEV uint32_t logit_key(float v) {
     uint32_t u = __float_as_uint(v);
     u = u == 0x80000000u ? 0u : u;
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (uint32_t)~id;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// (value desc, id asc): does candidate (va, ia) come before (vb, ib)? Bitwise, not
-// short-circuit: the logical form compiles to an exec-mask branch per comparison, which
-// made the 32-way rank take over a microsecond.
-DIH_DEV bool before(float va, uint32_t ia, float vb, uint32_t ib) {
-    return (va > vb) | ((va == vb) & (ia < ib));
+// Wave-uniform value of VGPR `v` in lane `l`.
+DIH_DEV uint32_t lane_value(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+
+// 64-bit rank key of expert `id`'s logit: a larger key comes first in (value desc, id asc)
+// order. Slots past the expert count get key (0, ~id): distinct, and behind every expert.
+DIH_DEV unsigned long long rank_key(float v, uint32_t id, bool expert) {
+    return ((unsigned long long)(expert ? logit_key(v) : 0u) << 32) | (uint32_t)~id;
+}
+
+// Sum of `r` over the four lanes of each quad (DPP quad permutes, no LDS).
+DIH_DEV int quad_sum(int r) {
+    r += __builtin_amdgcn_mov_dpp(r, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    r += __builtin_amdgcn_mov_dpp(r, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    return r;
 }
 
 }  // namespace
@@ -228,7 +236,6 @@ struct DecodeParams {
     const uint32_t *rp; const uint16_t *rs, *rb;           // router [E, H], 8-bit (or null)
     const float *logits_in;                                 // supplied logits [E] (router null)
     float *logits;                                          // router logits out [E]
-    float2 *cand;                                           // [nchunks * 8] (value, id bits)
     const uint32_t *sgp, *sup; const uint16_t *sgs, *sgb, *sus, *sub;  // shared gate/up [I, H]
     const uint32_t *srp; const uint16_t *srs, *srb;         // shared route [1, H], 8-bit
     float *sact;                                            // [I]
@@ -244,7 +251,7 @@ struct DecodeParams {
     float *route_out;                                       // optional [9, H]
     int E, H, I;
     int lpr_h, lpr_i;
-    int nchunks;          // router blocks (ceil(E / 32))
+    int nchunks;          // router blocks (ceil(E / (kK1Waves * rows per wave)))
     int shared_blocks;    // K1 blocks for the shared gate/up
     int gate_blocks;      // K2 blocks per slot
     int down_rows;        // K3 output rows per block
@@ -258,15 +265,14 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
     __shared__ float xsl[64];
     __shared__ __align__(16) uint32_t xh[1024];
     __shared__ float xhs[64], xhm[64];
-    __shared__ __align__(16) float lg[kChunkExperts];
-    __shared__ __align__(16) unsigned long long lkey[kChunkExperts];
     const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     if (b < P.nchunks) {
-        // router rows b*16 + wave*4*rpw + q*rpw + g (8-bit); rows past the chunk are masked
+        // router rows b*chunk + wave*rpw + g (8-bit), one row group a wave
+        const int chunk = kK1Waves * kRouterGroups * L.rpw;
         const int wrow = wave * kRouterGroups * L.rpw;
-        const int base = b * kChunkExperts + wrow;
-        const int n = min(kChunkExperts, P.E - b * kChunkExperts);
+        const int base = b * chunk + wrow;
+        const int n = min(chunk, P.E - b * chunk);
         if (P.rp) {
             const uint4 xv = stage_x_load(P.x, P.H);
             Rows<8, kRouterGroups> R;
@@ -280,49 +286,11 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
             rows_dot_h8<kRouterGroups>(R, xr, xs, mult, L.valid, L.lpr, v);
 #pragma unroll
             for (int q = 0; q < kRouterGroups; q++) {
-                const int o = wrow + q * L.rpw + L.g;  // row within the chunk
-                if (L.j == 0 && o < n) {
-                    lg[o] = v[q];
-                    lkey[o] = rank_key(v[q], (uint32_t)(b * kChunkExperts + o));
-                }
+                const int o = wrow + q * L.rpw + L.g;  // row within the block's experts
+                if (L.j == 0 && o < n) P.logits[b * chunk + o] = v[q];
             }
-        } else if (threadIdx.x < kChunkExperts) {
-            const int e = b * kChunkExperts + threadIdx.x;
-            if ((int)threadIdx.x < n) {
-                lg[threadIdx.x] = P.logits_in[e];
-                lkey[threadIdx.x] = rank_key(lg[threadIdx.x], (uint32_t)e);
-            }
-        }
-        // entries past the last expert rank after every real one
-        if (threadIdx.x < kChunkExperts && (int)threadIdx.x >= n) {
-            lg[threadIdx.x] = -INFINITY;
-            lkey[threadIdx.x] = rank_key(-INFINITY, 0xffffff00u + threadIdx.x);
-        }
-        __syncthreads();
-        if (wave == 0) {
-            // rank of each of the chunk's logits: lanes c, c+16, c+32, c+48 each count the
-            // keys of one quarter of the chunk that order before candidate c (broadcast LDS
-            // reads, one 64-bit compare per key); the eight first become candidates
-            const int c = lane & 15, quarter = lane >> 4;
-            const unsigned long long me = lkey[c];
-            int rank = 0;
-#pragma unroll
-            for (int k = 0; k < kChunkExperts / 4; k += 2) {
-                const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&lkey[quarter * (kChunkExperts / 4) + k]);
-                rank += q.x > me ? 1 : 0;
-                rank += q.y > me ? 1 : 0;
-            }
-            rank += __shfl_xor(rank, 16, 64);
-            rank += __shfl_xor(rank, 32, 64);
-            const bool mine = lane < n;
-            const float v = lg[c];
-            const uint32_t id = (uint32_t)(b * kChunkExperts + c);
-            const bool bad = __any(mine && !isfinite(v));
-            if (lane < kChunkExperts && rank < 8)
-                P.cand[b * 8 + rank] = make_float2(v, __uint_as_float(bad ? 0xfffffffeu : (lane < n ? id : 0xffffff00u + (uint32_t)c)));
-            // the logits go out after the barriers: a global store before a barrier would
-            // hold every wave until the store completes
-            if (mine) P.logits[b * kChunkExperts + lane] = v;
+        } else if ((int)threadIdx.x < n) {
+            P.logits[b * chunk + threadIdx.x] = P.logits_in[b * chunk + threadIdx.x];
         }
         return;
     }
@@ -374,64 +342,82 @@ __global__ __launch_bounds__(kWaves * 64) void decode_experts_kernel(DecodeParam
     __shared__ float xsl[BITS == 8 ? 1 : 64];
     __shared__ __align__(16) uint32_t xh[BITS == 8 ? 1024 : 1];
     __shared__ float xhs[BITS == 8 ? 64 : 1], xhm[BITS == 8 ? 64 : 1];
-    __shared__ __align__(16) float2 cl[kMaxCand];
-    __shared__ int rk[kMaxCand];
-    __shared__ uint32_t chosen[8];
-    __shared__ float chosen_v[8];
+    __shared__ __align__(16) unsigned long long ck[kMaxExperts];
+    __shared__ float cv[kMaxExperts];
+    __shared__ __align__(16) unsigned long long cm[64];
+    __shared__ int rk[64];
     __shared__ int any_bad;
-    const int t = threadIdx.x, wave = t >> 6;
+    static_assert(kWaves * 64 == 4 * kMaxExperts && kWaves * 4 == 64, "rank layout");
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int slot = blockIdx.x / P.gate_blocks;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     const int base = ((blockIdx.x - slot * P.gate_blocks) * kWaves + wave) * L.rpw;
-    // candidates -> rank -> this slot's expert, ranked once per block: thread t compares
-    // candidate t%128 with the candidates of part t/128 of kWaves/2 parts (slots past nc
-    // hold (-inf, 0xffffffff), which no candidate ranks behind)
-    const int nc = P.nchunks * 8;
-    if (t < kMaxCand) {
-        cl[t] = t < nc ? P.cand[t] : make_float2(-INFINITY, __uint_as_float(0xffffffffu));
-        rk[t] = 0;
+    // The token's experts, ranked once per block in two rounds on 64-bit keys (value desc,
+    // id asc, as the reference's insertion with `>`, SelectExperts Qwen36Model.cs:246-261):
+    // each group of 32 logits keeps its top-8 (four lanes a logit, eight comparisons each),
+    // then the 64 kept are ranked by all 16 waves (four comparisons a lane).
+    if (t < kMaxExperts) {
+        const bool ex = t < P.E;
+        const float v = ex ? P.logits[t] : 0.f;
+        ck[t] = rank_key(v, (uint32_t)t, ex);
+        cv[t] = v;
+        if (t < 64) rk[t] = 0;
         if (t == 0) any_bad = 0;
     }
     if constexpr (BITS == 8) stage_xh_store(stage_x_load(P.x, P.H), P.H, xh, xhs, xhm);
     else stage_x_store(stage_x_load(P.x, P.H), P.H, xl, xsl);
     __syncthreads();
     {
-        const int c = t & (kMaxCand - 1), g = t / kMaxCand;
-        const float2 me = cl[c];
-        const uint32_t mid = __float_as_uint(me.y);
+        const int c = t >> 2, p = t & 3, grp = c >> 5;
+        const unsigned long long me = ck[c];
+        const unsigned long long *q = &ck[grp * 32 + p * 8];
         int r = 0;
-        constexpr int kPart = kMaxCand / (kWaves / 2);
 #pragma unroll
-        for (int k = 0; k < kPart; k += 2) {
-            const float4 q = *reinterpret_cast<const float4 *>(&cl[g * kPart + k]);
-            r += before(q.x, __float_as_uint(q.y), me.x, mid) ? 1 : 0;
-            r += before(q.z, __float_as_uint(q.w), me.x, mid) ? 1 : 0;
+        for (int k = 0; k < 8; k++) r += q[k] > me ? 1 : 0;
+        r = quad_sum(r);
+        if (p == 0) {
+            if (r < 8) cm[grp * 8 + r] = me;
+            if (c < P.E && !isfinite(cv[c])) any_bad = 1;
         }
-        if (r) atomicAdd(&rk[c], r);
-        if (g == 0 && c < nc && mid == 0xfffffffeu) any_bad = 1;
     }
     __syncthreads();
-    if (t < nc && rk[t] < 8) {
-        chosen[rk[t]] = __float_as_uint(cl[t].y);
-        chosen_v[rk[t]] = cl[t].x;
+    {
+        const unsigned long long me = cm[lane];
+        int r = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) r += cm[wave * 4 + k] > me ? 1 : 0;
+        if (r) atomicAdd(&rk[lane], r);
     }
     __syncthreads();
+    // kept key `lane` has rank rk[lane]; the low word of a key is ~id
+    const int myrank = rk[lane];
+    const uint32_t myid = ~(uint32_t)cm[lane];
     const bool bad = any_bad != 0;
-    const uint32_t e = bad ? 0u : chosen[slot];
+    const uint32_t e = bad ? 0u : lane_value(myid, __ffsll((long long)__ballot(myrank == slot)) - 1);
     // one gated row group of expert e per wave
     const size_t ebase = (size_t)e * P.I;
     Rows<BITS, 1> G, U;
     rows_load<BITS, 1>(G, P.gp, P.gs, P.gb, ebase, P.I, base, L.rpw, L.g, L.jc, P.H);
     rows_load<BITS, 1>(U, P.upp, P.us, P.ub, ebase, P.I, base, L.rpw, L.g, L.jc, P.H);
-    if (blockIdx.x == 0 && t == 0) {
-        // softmax over the eight chosen logits, the first (largest) subtracted, summed in
-        // slot order (Softmax Qwen36Model.cs:293-298)
-        float p[8], total = 0.f;
+    if (blockIdx.x == 0 && wave == 0) {
+        // lane s < 8 publishes slot s: softmax over the eight chosen logits, the first
+        // (largest) subtracted, summed in slot order (Softmax Qwen36Model.cs:293-298)
+        uint32_t sid = 0;
 #pragma unroll
-        for (int s = 0; s < 8; s++) { p[s] = __expf(chosen_v[s] - chosen_v[0]); total += p[s]; }
+        for (int s = 0; s < 8; s++) {
+            const uint32_t id = lane_value(myid, __ffsll((long long)__ballot(myrank == s)) - 1);
+            sid = lane == s ? id : sid;
+        }
+        const float sv = cv[sid];
+        const float v0 = __uint_as_float(lane_value(__float_as_uint(sv), 0));
+        float total = 0.f;
 #pragma unroll
-        for (int s = 0; s < 8; s++) { P.ids[s] = bad ? 0u : chosen[s]; P.probs[s] = p[s] / total; }
-        if (bad && P.status) *P.status = 1u;
+        for (int s = 0; s < 8; s++) total += __expf(__uint_as_float(lane_value(__float_as_uint(sv), s)) - v0);
+        if (lane < 8) {
+            P.ids[lane] = bad ? 0u : sid;
+            P.probs[lane] = __expf(sv - v0) / total;
+        }
+        if (lane == 0 && bad && P.status) *P.status = 1u;
     }
     float a[1], u[1];
     if constexpr (BITS == 8) {
@@ -541,7 +527,7 @@ bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix 
     const int E = gate->experts, H = gate->columns, I = gate->rows;
     return (!router || router->bits == 8) && sr->bits == 8 && sg->bits == gate->bits &&
            sd->bits == gate->bits && down->bits == gate->bits && sg->rows == I && sd->columns == I &&
-           H <= 2048 && I <= 1024 && E <= 256 && (gate->bits == 8 || gate->bits == 5);
+           H <= 2048 && I <= 1024 && E <= kMaxExperts && (gate->bits == 8 || gate->bits == 5);
 }
 
 bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int capacity) {
@@ -553,7 +539,6 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
     if (a.router) { P.rp = a.router->packed(); P.rs = a.router->scales(); P.rb = a.router->biases(); }
     P.logits_in = a.logits_in;
     P.logits = a.logits;
-    P.cand = a.cand;
     P.sgp = a.shared_gate->packed(); P.sgs = a.shared_gate->scales(); P.sgb = a.shared_gate->biases();
     P.sup = a.shared_up->packed(); P.sus = a.shared_up->scales(); P.sub = a.shared_up->biases();
     P.srp = a.shared_route->packed(); P.srs = a.shared_route->scales(); P.srb = a.shared_route->biases();
@@ -564,8 +549,8 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
     P.sdp = a.shared_down->packed(); P.sds = a.shared_down->scales(); P.sdb = a.shared_down->biases();
     P.act = a.act; P.ids = a.ids; P.probs = a.probs; P.status = a.status;
     P.x = a.x; P.residual = a.residual; P.residual_f32 = a.residual_f32; P.route_out = a.route_out;
-    P.nchunks = (P.E + kChunkExperts - 1) / kChunkExperts;
     const int rpw = 64 / P.lpr_h;
+    P.nchunks = (P.E + kK1Waves * kRouterGroups * rpw - 1) / (kK1Waves * kRouterGroups * rpw);
     P.shared_blocks = (P.I + kK1Waves * rpw - 1) / (kK1Waves * rpw);
     P.gate_blocks = (P.I + kWaves * rpw - 1) / (kWaves * rpw);
     P.down_rows = std::min(64, kDownGroups * (64 / P.lpr_i));

@@ -67,7 +67,7 @@ struct Context {
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_CAND, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_W16, S_BLASWS, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_W16, S_BLASWS, S_COUNT_
 };
 static_assert(S_COUNT_ <= (int)(sizeof(Context::ws) / sizeof(Scratch)), "scratch table too small");
 
@@ -176,16 +176,15 @@ bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens,
                       const float *route_out, const float *probs, void *residual,
                       const MergeOut &mo, hipStream_t s, char *error, int capacity);
 
-// Decode MoE step in three launches (decode.hip). Device buffers: logits [E], cand
-// [ceil(E/32)*8] float2, sact [I], sroute [1], act [8*I], ids [8], probs [8], status [1]
-// (may be null), route_out [9*H] (may be null).
+// Decode MoE step in three launches (decode.hip). Device buffers: logits [E], sact [I],
+// sroute [1], act [8*I], ids [8], probs [8], status [1] (may be null), route_out [9*H]
+// (may be null).
 struct DecodeLaunch {
     const Matrix *router = nullptr, *gate = nullptr, *up = nullptr, *down = nullptr;
     const Matrix *shared_gate = nullptr, *shared_up = nullptr, *shared_down = nullptr;
     const Matrix *shared_route = nullptr;
     const float *logits_in = nullptr;
     float *logits = nullptr;
-    float2 *cand = nullptr;
     float *sact = nullptr, *sroute = nullptr, *act = nullptr;
     uint32_t *ids = nullptr;
     float *probs = nullptr;

@@ -408,6 +408,60 @@ def test_moe_decode_with_supplied_logits(device):
                 m.dispose()
 
 
+@pytest.mark.parametrize("E", [8, 37, 200, 256])
+def test_moe_decode_routing_ties_and_expert_counts(device, E):
+    """Decode routing for expert counts that fill the router blocks partly, with heavy exact
+    ties (and -0 against +0) in supplied logits, against the reference rule (largest, ties
+    to the lowest index); a router computed on the GPU for the same counts; and a NaN
+    logit, which fails the step with status 1 (Qwen36Model.cs:252)."""
+    rng = np.random.default_rng(40 + E)
+    H, I = 512, 256
+    L = _moe_layer(rng, E, H, I, 8)
+    q, layer = _upload_layer(device, L)
+    layer_s = dh.make_layer(None, *q[1:])  # the same weights, logits supplied
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=H).astype(np.float32))
+        for trial in range(3):
+            lg = rng.choice(np.array([-1.5, -0.0, 0.0, 0.25, 2.0], dtype=np.float32), size=E)
+            if trial == 2:
+                lg[:] = 0.0
+                lg[1::2] = -0.0
+            ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+            probs = torch.zeros(8, dtype=torch.float32, device="cuda")
+            status = torch.zeros(1, dtype=torch.int32, device="cuda")
+            res = torch.zeros(H, dtype=torch.int16, device="cuda")
+            dh.moe_decode(device, layer_s, dev_bf16(xb), res, logits=torch.from_numpy(lg).cuda(),
+                          trace=dh.make_trace(ids=ids, probs=probs, status=status))
+            torch.cuda.synchronize()
+            oid, opr = orc.top8(lg)
+            assert np.array_equal(ids.cpu().numpy(), oid), (trial, ids.cpu().numpy(), oid)
+            assert np.max(np.abs(probs.cpu().numpy() - opr)) <= 1e-6
+            assert int(status.item()) == 0
+        # the router on the GPU
+        lgt = torch.zeros(E, dtype=torch.float32, device="cuda")
+        ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+        dh.moe_decode(device, layer, dev_bf16(xb), torch.zeros(H, dtype=torch.int16, device="cuda"),
+                      trace=dh.make_trace(logits=lgt, ids=ids))
+        torch.cuda.synchronize()
+        got_lg = lgt.cpu().numpy()
+        assert orc.rel_err(got_lg, orc.qmv_f64(L.router, orc.bf16_bits_to_f32(xb))) < 1e-5
+        assert np.array_equal(ids.cpu().numpy(), orc.top8(got_lg)[0])
+        # a NaN logit: status 1 and ids 0
+        lg = rng.normal(size=E).astype(np.float32)
+        lg[E // 2] = np.nan
+        ids = torch.full((8,), 7, dtype=torch.int32, device="cuda")
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        dh.moe_decode(device, layer_s, dev_bf16(xb), torch.zeros(H, dtype=torch.int16, device="cuda"),
+                      logits=torch.from_numpy(lg).cuda(), trace=dh.make_trace(ids=ids, status=status))
+        torch.cuda.synchronize()
+        assert int(status.item()) == 1
+        assert not ids.cpu().numpy().any()
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
 def _zipf_logits(rng, T, E, s=1.1):
     """Router logits log p_e + Gumbel with p ~ rank^-s: top-8 = Zipf sampling without
     replacement (config 3)."""

@@ -312,6 +312,80 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     }
 }
 
+// One-shot GEMV for long single-matrix launches of 8-bit rows of 2048 columns with bf16
+// activations and no expert ids (the lm_head): wave w computes rows kStreamRows*w ..
+// kStreamRows*w + kStreamRows - 1 of its slot and exits. Lane l owns columns 32l .. 32l+31
+// of every row and stages its own activations in registers (f16, scaled by a power of two
+// as in xstage_store): no LDS and no barrier, so a block is only its waves' loads in
+// flight, and the launch is many short blocks rather than a resident set walking rows.
+// Measured on the lm_head (248,320 rows, plain loads): 83 us against 97 us for the
+// resident qmv_kernel; 1, 2, 4 and 8 rows a wave took 131, 85, 88 and 87 us, two- and
+// eight-wave blocks 85 us, non-temporal loads 99 us. On a 4096-row GEMV the kernel is
+// faster (4.2 against 4.6 us) but the launch of 342 blocks makes the step slower.
+constexpr int kStreamRows = 3;
+
+__global__ __launch_bounds__(256) void qmv_stream_kernel(QmvParams P) {
+    const int blk = blockIdx.x;
+    int k = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxSeg; i++)
+        if (i < P.nseg && blk >= P.start[i]) k = i;
+    const QmvSeg &S = P.seg[k];
+    const int local = blk - P.start[k];
+    const int slot = local / P.blocks_per_slot[k];
+    const int r0 = ((local - slot * P.blocks_per_slot[k]) * 4 + (threadIdx.x >> 6)) * kStreamRows;
+    const int lane = threadIdx.x & 63;
+    const uint4 *xp = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(S.x) + (size_t)slot * S.x_slot_stride) + lane * 4;
+    uint4 xv[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) xv[q] = xp[q];
+    Chunk<8> w[kStreamRows];
+    uint32_t sc[kStreamRows], bi[kStreamRows];
+#pragma unroll
+    for (int q = 0; q < kStreamRows; q++) {
+        const int r = min(r0 + q, S.rows - 1);
+        load_chunk<8, false>(w[q], S.p0 + (size_t)r * 512, lane);
+        sc[q] = S.s0[(size_t)r * 32 + (lane >> 1)];
+        bi[q] = S.b0[(size_t)r * 32 + (lane >> 1)];
+    }
+    float f[32];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t u[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            f[8 * q + 2 * m] = __uint_as_float(u[m] << 16);
+            f[8 * q + 2 * m + 1] = __uint_as_float(u[m] & 0xffff0000u);
+        }
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(f[i]));
+    const int ex = (int)((__float_as_uint(mx) >> 23) & 255u) - 126;
+    const int scl = max(ex - 15, -100);   // (an all-zero chunk: any scale)
+    uint32_t xq[16];
+    float xs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const _Float16 h0 = (_Float16)ldexpf(f[2 * i], -scl), h1 = (_Float16)ldexpf(f[2 * i + 1], -scl);
+        xs += (float)h0 + (float)h1;
+        xq[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    }
+    const float mult = __uint_as_float((uint32_t)(127 + scl) << 23);
+#pragma unroll
+    for (int q = 0; q < kStreamRows; q++) {
+        const float d = chunk_dot_h8(w[q], xq) - 1024.f * xs;
+        const float v = wave_sum(mult * (bf16_to_f32(sc[q]) * d + bf16_to_f32(bi[q]) * xs));
+        if (lane == 0 && r0 + q < S.rows) {
+            const size_t o = (size_t)slot * S.rows + r0 + q;
+            if (S.y_bf16)
+                static_cast<uint16_t *>(S.y)[o] = f32_to_bf16(v);
+            else
+                static_cast<float *>(S.y)[o] = v;
+        }
+    }
+}
+
 static int pow2ceil(int v) {
     int p = 1;
     while (p < v) p <<= 1;
@@ -344,9 +418,10 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
         total += groups[i] * segs[i].count;
     }
     // Row groups per wave: one while the launch has at most kWavesTarget row groups,
-    // else enough that the waves number about kWavesTarget. Long launches (the lm_head's
-    // 248,320 rows) run the single-matrix kernel instance (102 VGPRs: four waves per SIMD,
-    // so all kWavesTarget waves are resident at once, no trailing partial round).
+    // else enough that the waves number about kWavesTarget. Long launches run the one-shot
+    // qmv_stream_kernel when their rows allow it (8-bit, 2048 columns, bf16 x, no expert
+    // ids: the lm_head), else the single-matrix kernel instance (102 VGPRs: four waves per
+    // SIMD, so all kWavesTarget waves are resident at once, no trailing partial round).
     const bool longrun = total > 4L * kWavesTarget;
     const long per = std::max(1L, (total + kWavesTarget - 1) / kWavesTarget);
     int kmax = 1;
@@ -376,11 +451,25 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
     int maxc = 0;
     for (int i = 0; i < nseg; i++) maxc = std::max(maxc, segs[i].columns);
     const uint32_t lds = (uint32_t)maxc * 4 + (uint32_t)(maxc / 32) * 8;
-    // plain loads and the single-matrix instance for long four-deep launches (measured
-    // 107 -> 98 us on the lm_head; plain loads are 5 % slower on a 4096-row GEMV and equal
-    // on the decode step)
+    // plain loads and the single-matrix instance for the other long four-deep launches
+    // (measured 107 -> 98 us on the lm_head before the one-shot kernel; plain loads are 5 %
+    // slower on a 4096-row GEMV and equal on the decode step)
     bool plain = longrun && depth == 4 && cpl == 1;
     for (int i = 0; i < nseg; i++) plain = plain && !segs[i].p1;
+    bool stream = plain && bits == 8;
+    for (int i = 0; i < nseg; i++)
+        stream = stream && segs[i].columns == 2048 && segs[i].x_bf16 && !segs[i].ids && !segs[i].top8;
+    if (stream) {
+        int b = 0;
+        for (int i = 0; i < nseg; i++) {
+            P.blocks_per_slot[i] = (segs[i].rows + 4 * kStreamRows - 1) / (4 * kStreamRows);
+            P.start[i] = b;
+            b += P.blocks_per_slot[i] * segs[i].count;
+        }
+        P.start[nseg] = b;
+        DIH_LAUNCH((qmv_stream_kernel), dim3(b), dim3(256), 0, s, P);
+        return hip_ok(hipGetLastError(), error, capacity, "qmv launch");
+    }
     if (plain) {
         if (bits == 8) DIH_LAUNCH((qmv_kernel<8, 1, 4, true>), grid, block, lds, s, P);
         else DIH_LAUNCH((qmv_kernel<5, 1, 4, true>), grid, block, lds, s, P);

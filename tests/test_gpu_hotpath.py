@@ -80,6 +80,35 @@ def test_qmv_bf16_matches_fp64_oracle(device, bits, rows, columns):
         m.dispose()
 
 
+@pytest.mark.parametrize("bits,x_bf16", [(8, True), (8, False), (5, True)])
+def test_qmv_long_launch_matches_fp64_oracle(device, bits, x_bf16):
+    """Launches of more than 16,384 row groups take the long-run kernels: 8-bit rows of 2048
+    columns with bf16 x the one-shot kernel (three rows a wave; 16,391 rows leave a ragged
+    last block), the others the resident single-matrix kernel."""
+    rng = np.random.default_rng(9)
+    rows, columns = 16391, 2048
+    host = orc.random_matrix(rng, 1, rows, columns, bits)
+    m = upload(device, host)
+    try:
+        xf = rng.normal(size=columns).astype(np.float32)
+        if x_bf16:
+            xb = orc.f32_to_bf16_bits(xf)
+            x, xf, xd = dev_bf16(xb), orc.bf16_bits_to_f32(xb), dh.BF16
+        else:
+            x, xd = torch.from_numpy(xf).cuda(), dh.F32
+        want = orc.qmv_f64(host, xf)
+        y32 = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+        yb = torch.zeros(rows, dtype=torch.int16, device="cuda")
+        dh.qmv(device, m, x, y32, x_dtype=xd, y_dtype=dh.F32)
+        dh.qmv(device, m, x, yb, x_dtype=xd, y_dtype=dh.BF16)
+        torch.cuda.synchronize()
+        e32 = orc.rel_err(y32.cpu().numpy(), want)
+        assert e32 < 1e-5, e32
+        assert np.array_equal(yb.cpu().numpy().view(np.uint16), orc.f32_to_bf16_bits(y32.cpu().numpy()))
+    finally:
+        m.dispose()
+
+
 def _dynamic_range_x(rng, n, profile):
     """bf16 activations for the f16 staging checks: 'span' gives every element a random
     binade in 2^-20..2^15, so every 32-column chunk spans the whole range; 'tiny' is
@@ -93,18 +122,20 @@ def _dynamic_range_x(rng, n, profile):
     return orc.f32_to_bf16_bits(x.astype(np.float32))
 
 
+@pytest.mark.parametrize("rows", [4096, 16391])
 @pytest.mark.parametrize("profile", ["span", "tiny", "huge"])
-def test_qmv_f16_staging_dynamic_range(device, profile):
+def test_qmv_f16_staging_dynamic_range(device, profile, rows):
     """The 8-bit decode GEMV stages bf16 x as f16, each 32-column chunk scaled by the power
     of two that puts its largest magnitude in [2^14, 2^15). That is exact for every value
     within 2^29 of the chunk's largest, so the result stays at fp32-accumulation accuracy
-    whatever the activations' scale (config-1 shape)."""
+    whatever the activations' scale (config-1 shape; 16,391 rows: the one-shot long-launch
+    kernel, which stages per lane in registers)."""
     rng = np.random.default_rng(11)
-    host = orc.random_matrix(rng, 1, 4096, 2048, 8)
+    host = orc.random_matrix(rng, 1, rows, 2048, 8)
     m = upload(device, host)
     try:
         xb = _dynamic_range_x(rng, 2048, profile)
-        y = torch.zeros(4096, dtype=torch.float32, device="cuda")
+        y = torch.zeros(rows, dtype=torch.float32, device="cuda")
         dh.qmv(device, m, dev_bf16(xb), y, y_dtype=dh.F32)
         torch.cuda.synchronize()
         want = orc.qmv_f64(host, orc.bf16_bits_to_f32(xb))

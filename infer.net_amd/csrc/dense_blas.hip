@@ -14,9 +14,10 @@
 // The GEMM: Y[T][R] = X[T][C] * W16[R][C]^T. In hipBLASLt's column-major terms that is
 // D (R x T, ld R) = op(A) * B with A = W16 as a C x R matrix (ld C) transposed and B = X as
 // a C x T matrix (ld C): the "TN" form. One hipBLASLt handle per context; the algorithm
-// for each (R, C, T, output type) is chosen on first use from the heuristic's top
-// candidates by timing each once (skipped, taking the heuristic's first, when the stream is
-// being captured into a graph), and kept.
+// for each (R, C, T, output type) is chosen on first use from the heuristic's first 16
+// candidates by timing three back-to-back runs of each after one untimed run (skipped,
+// taking the heuristic's first, when the stream is being captured into a graph), and kept.
+// (Sixteen candidates instead of four found a faster in_proj kernel: 171 -> 163 us.)
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -125,12 +126,12 @@ bool make_plan(Context *c, BlasState &b, int R, int C, int T, bool y_bf16, const
     hipblasLtMatmulPreference_t pref = nullptr;
     if (!blas_ok(hipblasLtMatmulPreferenceCreate(&pref), error, capacity, "preference")) return false;
     const uint64_t wmax = kMaxWorkspace;
-    hipblasLtMatmulHeuristicResult_t cand[4];
+    hipblasLtMatmulHeuristicResult_t cand[16];
     int n = 0;
     hipblasStatus_t st =
         hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wmax, sizeof(wmax));
     if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulAlgoGetHeuristic(b.handle, p.desc, p.la, p.lb, p.ld, p.ld, pref, 4, cand, &n);
+        st = hipblasLtMatmulAlgoGetHeuristic(b.handle, p.desc, p.la, p.lb, p.ld, p.ld, pref, 16, cand, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (!blas_ok(st, error, capacity, "heuristic")) return false;
     if (n < 1) {
@@ -152,9 +153,11 @@ bool make_plan(Context *c, BlasState &b, int R, int C, int T, bool y_bf16, const
                                 ws, cand[i].workspaceSize, s) != HIPBLAS_STATUS_SUCCESS)
                 continue;
             if (hipEventRecord(c->start, s) != hipSuccess) break;
-            if (hipblasLtMatmul(b.handle, p.desc, &alpha, w16, p.la, x, p.lb, &beta, y, p.ld, y, p.ld, &cand[i].algo,
-                                ws, cand[i].workspaceSize, s) != HIPBLAS_STATUS_SUCCESS)
-                continue;
+            bool okr = true;
+            for (int rep = 0; rep < 3 && okr; rep++)
+                okr = hipblasLtMatmul(b.handle, p.desc, &alpha, w16, p.la, x, p.lb, &beta, y, p.ld, y, p.ld, &cand[i].algo,
+                                      ws, cand[i].workspaceSize, s) == HIPBLAS_STATUS_SUCCESS;
+            if (!okr) continue;
             float ms = 0.f;
             if (hipEventRecord(c->stop, s) != hipSuccess || hipEventSynchronize(c->stop) != hipSuccess ||
                 hipEventElapsedTime(&ms, c->start, c->stop) != hipSuccess)

@@ -312,18 +312,17 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvParams P) {
     }
 }
 
-// One-shot GEMV for long single-matrix launches of 8-bit rows of 2048 columns with bf16
-// activations and no expert ids (the lm_head): wave w computes rows kStreamRows*w ..
-// kStreamRows*w + kStreamRows - 1 of its slot and exits. Lane l owns columns 32l .. 32l+31
+// One-shot GEMV for single-matrix launches of 8-bit rows of 2048 columns with bf16
+// activations and no expert ids (the lm_head, a single decode GEMV): wave w computes rows
+// R*w .. R*w + R - 1 of its slot and exits. Lane l owns columns 32l .. 32l+31
 // of every row and stages its own activations in registers (f16, scaled by a power of two
 // as in xstage_store): no LDS and no barrier, so a block is only its waves' loads in
 // flight, and the launch is many short blocks rather than a resident set walking rows.
-// Measured on the lm_head (248,320 rows, plain loads): 83 us against 97 us for the
-// resident qmv_kernel; 1, 2, 4 and 8 rows a wave took 131, 85, 88 and 87 us, two- and
-// eight-wave blocks 85 us, non-temporal loads 99 us. On a 4096-row GEMV the kernel is
-// faster (4.2 against 4.6 us) but the launch of 342 blocks makes the step slower.
-constexpr int kStreamRows = 3;
-
+// Rows a wave: three for long launches (the lm_head: 83 us against 97 us for the resident
+// qmv_kernel; 1, 2, 4 and 8 rows took 131, 85, 88 and 87 us, two- and eight-wave blocks
+// 85 us, non-temporal loads 99 us), two otherwise (a 4096-row GEMV: 4.47 us a call
+// against 5.29 us resident; one row 4.87, three 5.4).
+template <int R>
 __global__ __launch_bounds__(256) void qmv_stream_kernel(QmvParams P) {
     const int blk = blockIdx.x;
     int k = 0;
@@ -333,16 +332,16 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(QmvParams P) {
     const QmvSeg &S = P.seg[k];
     const int local = blk - P.start[k];
     const int slot = local / P.blocks_per_slot[k];
-    const int r0 = ((local - slot * P.blocks_per_slot[k]) * 4 + (threadIdx.x >> 6)) * kStreamRows;
+    const int r0 = ((local - slot * P.blocks_per_slot[k]) * 4 + (threadIdx.x >> 6)) * R;
     const int lane = threadIdx.x & 63;
     const uint4 *xp = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(S.x) + (size_t)slot * S.x_slot_stride) + lane * 4;
     uint4 xv[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) xv[q] = xp[q];
-    Chunk<8> w[kStreamRows];
-    uint32_t sc[kStreamRows], bi[kStreamRows];
+    Chunk<8> w[R];
+    uint32_t sc[R], bi[R];
 #pragma unroll
-    for (int q = 0; q < kStreamRows; q++) {
+    for (int q = 0; q < R; q++) {
         const int r = min(r0 + q, S.rows - 1);
         load_chunk<8, false>(w[q], S.p0 + (size_t)r * 512, lane);
         sc[q] = S.s0[(size_t)r * 32 + (lane >> 1)];
@@ -373,7 +372,7 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(QmvParams P) {
     }
     const float mult = __uint_as_float((uint32_t)(127 + scl) << 23);
 #pragma unroll
-    for (int q = 0; q < kStreamRows; q++) {
+    for (int q = 0; q < R; q++) {
         const float d = chunk_dot_h8(w[q], xq) - 1024.f * xs;
         const float v = wave_sum(mult * (bf16_to_f32(sc[q]) * d + bf16_to_f32(bi[q]) * xs));
         if (lane == 0 && r0 + q < S.rows) {
@@ -456,18 +455,21 @@ bool launch_qmv(const QmvSeg *segs, int nseg, int bits, const Top8Source *top8, 
     // slower on a 4096-row GEMV and equal on the decode step)
     bool plain = longrun && depth == 4 && cpl == 1;
     for (int i = 0; i < nseg; i++) plain = plain && !segs[i].p1;
-    bool stream = plain && bits == 8;
+    bool stream = bits == 8 && cpl == 1;
     for (int i = 0; i < nseg; i++)
-        stream = stream && segs[i].columns == 2048 && segs[i].x_bf16 && !segs[i].ids && !segs[i].top8;
+        stream = stream && !segs[i].p1 && segs[i].columns == 2048 && segs[i].x_bf16 && !segs[i].ids &&
+                 !segs[i].top8;
     if (stream) {
+        const int rows = longrun ? 3 : 2;
         int b = 0;
         for (int i = 0; i < nseg; i++) {
-            P.blocks_per_slot[i] = (segs[i].rows + 4 * kStreamRows - 1) / (4 * kStreamRows);
+            P.blocks_per_slot[i] = (segs[i].rows + 4 * rows - 1) / (4 * rows);
             P.start[i] = b;
             b += P.blocks_per_slot[i] * segs[i].count;
         }
         P.start[nseg] = b;
-        DIH_LAUNCH((qmv_stream_kernel), dim3(b), dim3(256), 0, s, P);
+        if (longrun) DIH_LAUNCH((qmv_stream_kernel<3>), dim3(b), dim3(256), 0, s, P);
+        else DIH_LAUNCH((qmv_stream_kernel<2>), dim3(b), dim3(256), 0, s, P);
         return hip_ok(hipGetLastError(), error, capacity, "qmv launch");
     }
     if (plain) {

@@ -552,7 +552,7 @@ def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
 
 @pytest.mark.parametrize("bits,rows,columns,T", [(8, 512, 2048, 256), (5, 300, 512, 130), (8, 129, 256, 65),
                                                  (8, 2048, 4096, 64), (8, 1000, 2048, 1), (5, 300, 512, 3),
-                                                 (8, 129, 4096, 4)])
+                                                 (8, 129, 4096, 4), (8, 1003, 2048, 3)])
 def test_dense_matches_oracle(device, bits, rows, columns, T):
     """Up to four tokens the projection runs as a batched fp32 GEMV (the reference's short-
     chunk kernels, gpu_prefill.mm:615-619, do not round operands); longer chunks use bf16

@@ -597,6 +597,17 @@ __global__ __launch_bounds__(256) void attn_decode_scores_kernel(AttnParams P) {
     }
 }
 
+// Largest of the tile maxima tm[8 * tt] for tt = first + g, first + g + 4, .. <= tile (L
+// of them at most): independent loads (indices past `tile` repeat it), so that they are all
+// in flight together rather than one round trip each.
+template <int L>
+DIH_DEV float tile_prefix_max(const float *tm, int first, int tile, int g) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < L; j++) m = fmaxf(m, tm[8 * min(first + g + 4 * j, tile)]);
+    return m;
+}
+
 template <bool QBF16, bool PREMAX>
 __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
     __shared__ __align__(16) uint16_t vt[4][kDim * kVtStride];   // per wave; its partial sums after
@@ -650,7 +661,10 @@ __global__ __launch_bounds__(256, 2) void attn_decode_kernel(AttnParams P) {
             const float4 *src = reinterpret_cast<const float4 *>(P.scores + ((ti0 + tile) * 32 + 8 * g + n) * 8);
             sv[0] = src[0];
             sv[1] = src[1];
-            for (int tt = first + g; tt <= tile; tt += 4) rmax = fmaxf(rmax, P.tmax[(ti0 + tt) * 8 + n]);
+            const float *tm = P.tmax + ti0 * 8 + n;
+            const int span = tile - first;   // earlier tiles of the rounding partition
+            rmax = span < 32 ? tile_prefix_max<8>(tm, first, tile, g)
+                 : span < 64 ? tile_prefix_max<16>(tm, first, tile, g) : tile_prefix_max<32>(tm, first, tile, g);
         }
     }
     // (rows 8..15 load nothing: a branch, so that their lanes are off for the loads)

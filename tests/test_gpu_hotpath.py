@@ -55,9 +55,12 @@ def rms(a) -> float:
 # ------------------------------------------------------------------------------ qmv
 
 @pytest.mark.parametrize("bits,rows,columns", [(8, 4096, 2048), (5, 4096, 2048), (8, 300, 512),
-                                               (5, 129, 4096), (8, 97, 192), (5, 64, 64)])
+                                               (5, 129, 4096), (8, 97, 192), (5, 64, 64),
+                                               (8, 5, 2048), (8, 4097, 2048)])
 def test_qmv_bf16_matches_fp64_oracle(device, bits, rows, columns):
-    """Config-1 shape (8-bit [4096x2048], x bf16 ~N(0,1), bf16 out) and tails/odd widths."""
+    """Config-1 shape (8-bit [4096x2048], x bf16 ~N(0,1), bf16 out) and tails/odd widths
+    (8-bit rows of 2048 columns take the one-shot kernel: 5 rows is one partial block, 4097
+    leaves one row in the last block)."""
     rng = np.random.default_rng(0)
     host = orc.random_matrix(rng, 1, rows, columns, bits)
     m = upload(device, host)

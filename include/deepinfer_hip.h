@@ -64,7 +64,10 @@ void dih_quant_residency_prepare(void *context);
 /* ---- matrices -------------------------------------------------------------------- */
 
 /* Replaces di_quant_matrix_create (quantized.mm:294-315). Checks 1<=experts<=256,
- * rows>=1, columns a multiple of 64 (at most 8192), bits 5 or 8, group 64. */
+ * rows>=1, columns a multiple of 64 (at most 8192), bits 5 or 8, group 64. A 5-bit matrix
+ * with columns a multiple of 512 also holds a second device copy of its codes in 128-row
+ * tile-major order (the prefill GEMM reads that one), which every write path below keeps
+ * current; its bytes count in dih_quant_residency_bytes. */
 void *dih_quant_matrix_create(void *context, int experts, int rows, int columns, int bits,
                               int group, char *error, int capacity);
 /* Replaces di_quant_matrix_buffer (quantized.mm:316-319). index 0 packed, 1 scales,
@@ -81,10 +84,13 @@ void dih_quant_matrix_destroy(void *matrix);
  * `index` at byte `offset` of the device copy directly, without a staging copy. */
 int dih_quant_matrix_write(void *matrix, int index, size_t offset, const void *source,
                            size_t bytes, char *error, int capacity);
-/* New: uploads a dirty staging buffer now and releases the host staging copy. */
+/* New: uploads a dirty staging buffer now and releases the host staging copy; also
+ * brings the tile-major copy of 5-bit codes up to date after writes through the
+ * dih_quant_matrix_device pointer. */
 int dih_quant_matrix_commit(void *matrix, char *error, int capacity);
 /* New: device pointer of buffer `index` (0 packed, 1 scales, 2 biases) for callers
- * that fill weights on the device; uploads a dirty staging copy first. */
+ * that fill weights on the device; uploads a dirty staging copy first. Codes of a 5-bit
+ * matrix written through it reach the prefill GEMM after dih_quant_matrix_commit. */
 void *dih_quant_matrix_device(void *matrix, int index);
 /* New: shape query; any out pointer may be NULL. */
 int dih_quant_matrix_shape(void *matrix, int *experts, int *rows, int *columns, int *bits);

@@ -85,6 +85,7 @@ bool sync_matrix(Matrix *m, char *error, int capacity) {
                         capacity, "weight upload"))
                 return false;
             m->dirty[i] = false;
+            if (i == 0 && !matrix_retile(m, 0, (size_t)m->experts * m->rows, error, capacity)) return false;
         }
     }
     return true;
@@ -277,7 +278,19 @@ __attribute__((visibility("default"))) void *dih_quant_matrix_create(void *ctx, 
             return nullptr;
         }
     }
-    c->weight_bytes += m->bytes[0] + m->bytes[1] + m->bytes[2];
+    // 5-bit matrices the streaming GEMM can take get the tile-major copy of their codes
+    // (zeros, like the codes, until written)
+    if (bits == 5 && columns % 512 == 0) {
+        m->tiled_bytes = (size_t)experts * m->tiled_rows() * columns * bits / 8;
+        if (hipMalloc(&m->tiled, m->tiled_bytes) != hipSuccess || hipMemset(m->tiled, 0, m->tiled_bytes) != hipSuccess) {
+            if (m->tiled) (void)hipFree(m->tiled);
+            for (int j = 0; j < 3; j++) (void)hipFree(m->dev[j]);
+            delete m;
+            set_error(error, capacity, "Quantized buffer allocation failed");
+            return nullptr;
+        }
+    }
+    c->weight_bytes += m->bytes[0] + m->bytes[1] + m->bytes[2] + m->tiled_bytes;
     return m;
 }
 
@@ -301,11 +314,12 @@ __attribute__((visibility("default"))) void dih_quant_matrix_destroy(void *matri
     Matrix *m = as_mat(matrix);
     if (!m) return;
     (void)hipDeviceSynchronize();
-    if (m->ctx) m->ctx->weight_bytes -= m->bytes[0] + m->bytes[1] + m->bytes[2];
+    if (m->ctx) m->ctx->weight_bytes -= m->bytes[0] + m->bytes[1] + m->bytes[2] + m->tiled_bytes;
     for (int i = 0; i < 3; i++) {
         if (m->dev[i]) (void)hipFree(m->dev[i]);
         if (m->host[i]) (void)hipHostFree(m->host[i]);
     }
+    if (m->tiled) (void)hipFree(m->tiled);
     if (m->stage_in) (void)hipFree(m->stage_in);
     if (m->stage_out) (void)hipFree(m->stage_out);
     m->magic = 0;
@@ -325,6 +339,10 @@ __attribute__((visibility("default"))) int dih_quant_matrix_write(void *matrix, 
     if (!hip_ok(hipMemcpy(static_cast<char *>(m->dev[index]) + offset, source, bytes, hipMemcpyDefault),
                 error, capacity, "weight upload"))
         return -1;
+    if (index == 0 && bytes > 0) {  // the code rows the write touched
+        const size_t rb = m->words_per_row() * 4, r0 = offset / rb, r1 = (offset + bytes - 1) / rb + 1;
+        if (!matrix_retile(m, r0, r1 - r0, error, capacity)) return -1;
+    }
     if (m->host[index] && hipMemcpy(static_cast<char *>(m->host[index]) + offset, static_cast<char *>(m->dev[index]) + offset,
                                      bytes, hipMemcpyDeviceToHost) != hipSuccess) {
         set_error(error, capacity, "staging refresh failed");
@@ -340,6 +358,8 @@ __attribute__((visibility("default"))) int dih_quant_matrix_commit(void *matrix,
         return -1;
     }
     if (!sync_matrix(m, error, capacity)) return -1;
+    // codes written through the device pointer reach the tile-major copy here
+    if (!matrix_retile(m, 0, (size_t)m->experts * m->rows, error, capacity)) return -1;
     for (int i = 0; i < 3; i++)
         if (m->host[i]) {
             (void)hipHostFree(m->host[i]);

@@ -24,6 +24,13 @@ struct Matrix {
     size_t bytes[3] = {0, 0, 0};
     float *stage_in = nullptr, *stage_out = nullptr;  // f32 staging for host-pointer calls
     size_t stage_in_bytes = 0, stage_out_bytes = 0;
+    // 5-bit matrices with K a multiple of 512: a second copy of the codes in 128-row
+    // tile-major order, [expert][row tile][K step][row in tile][40 bytes], rows padded to
+    // a multiple of 128 with zeros, read by the streaming grouped/dense GEMM (one K step of
+    // a row tile is then 5,120 contiguous bytes instead of 128 40-byte pieces 1,280 bytes
+    // apart). Kept equal to dev[0] by every write path (matrix_retile).
+    void *tiled = nullptr;
+    size_t tiled_bytes = 0;
     uint32_t magic = 0x44494d58u;
 
     const uint32_t *packed() const { return static_cast<const uint32_t *>(dev[0]); }
@@ -31,6 +38,7 @@ struct Matrix {
     const uint16_t *biases() const { return static_cast<const uint16_t *>(dev[2]); }
     size_t words_per_row() const { return (size_t)columns * bits / 32; }
     size_t groups_per_row() const { return (size_t)columns / 64; }
+    size_t tiled_rows() const { return ((size_t)rows + 127) / 128 * 128; }  // per expert
 };
 
 // Grow-only device scratch buffer.
@@ -76,6 +84,9 @@ void set_error(char *error, int capacity, const std::string &message);
 bool hip_ok(hipError_t e, char *error, int capacity, const char *what);
 void *ctx_scratch(Context *c, ScratchId id, size_t bytes, char *error, int capacity);
 bool sync_matrix(Matrix *m, char *error, int capacity);
+// Rewrites the tile-major copy of flattened code rows [first, first + count) (row index
+// expert * rows + row) from dev[0]; no work for matrices without one. Host-synchronous.
+bool matrix_retile(Matrix *m, size_t first, size_t count, char *error, int capacity);
 
 // Profiling. While a ProfScope for a profiling context is alive on this thread, every
 // launch goes through hipExtLaunchKernelGGL with a start/stop event pair taken from the

@@ -448,6 +448,11 @@ Matrix *ck_matrix(Checkpoint &c, Context *ctx, const std::string &prefix, int ro
             return nullptr;
         }
     }
+    if (!matrix_retile(m, 0, (size_t)m->experts * m->rows, e, sizeof(e))) {
+        dih_quant_matrix_destroy(m);
+        f.set(kInvalid, e);
+        return nullptr;
+    }
     return m;
 }
 

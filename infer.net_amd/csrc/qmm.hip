@@ -385,13 +385,17 @@ constexpr int qmm_lds_occupancy() {
 // RS (dense only): 32-row slabs per wave, so a block's row tile is 128*RS rows. Two slabs
 // double the MFMA work per activation tile read from LDS (each wave reads the whole tile
 // every step), which otherwise costs as much LDS bandwidth as the MFMAs take time.
-template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1>
+// TL: the codes come from the matrix's 128-row tile-major copy (5-bit): a K step of 128 rows
+// is one contiguous 5,120-byte block, so each dword copy instruction of a wave reads 256
+// contiguous bytes instead of pieces of six or seven rows 1,280 bytes apart.
+template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1, bool TL = false>
 __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
     // 32-route tiles (NT = 1) gave wrong results in the 8-bit grouped down projection, cause
     // not found (the copy and operand index arithmetic checks out on the host): not built
     static_assert(NT >= 2, "route tiles of 64 or more routes only");
     static_assert(!SPLIT || GATED, "only the gated kernel splits its matrices over waves");
     static_assert(RS == 1 || (!GATED && !SPLIT), "two slabs a wave: non-gated only");
+    static_assert(!TL || BITS == 5, "tile-major codes: 5-bit only");
     constexpr int TR = 128 * RS;             // rows per row tile
     constexpr int NW = SPLIT ? 8 : 4;        // waves per block
     constexpr int BN = 32 * NT;
@@ -521,18 +525,40 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
 
     // Copy sources: the expert's first row in each matrix (wave-uniform) plus a 32-bit lane
     // offset of the row within the expert (an expert's rows span less than 2^31 bytes, checked
-    // on the host); a K step adds the wave-uniform offset kg * AB. The issue position (the
-    // next step to copy, as tile and K step) is wave-uniform, so the step bookkeeping is scalar
-    // and no step index is divided at run time.
+    // on the host); a K step adds the wave-uniform offset kg * KSTEP. Row-major codes: a row
+    // starts row * row_bytes in, a K step is AB bytes further. Tile-major codes (experts padded
+    // to whole 128-row tiles): a 128-row tile starts tile * 128 * row_bytes in, its row rr
+    // rr * AB further, and a K step is 128 * AB bytes. The issue position (the next step to
+    // copy, as tile and K step) is wave-uniform, so the step bookkeeping is scalar and no step
+    // index is divided at run time.
+    constexpr uint32_t KSTEP = TL ? 128 * AB : AB;
+    const size_t wrows = TL ? (size_t)((R + 127) & ~127) : (size_t)R;  // code rows per expert
     const char *wbase[WMAT];
 #pragma unroll
-    for (int mm = 0; mm < WMAT; mm++) wbase[mm] = pw[mm + mw] + ebase * row_bytes;
-    uint32_t woff[AQ];
-    auto set_tile = [&](int ti) {
+    for (int mm = 0; mm < WMAT; mm++) wbase[mm] = pw[mm + mw] + (size_t)(shared ? 0 : e) * wrows * row_bytes;
+    // Tile-major: the lane's offset within a row tile's first K step is fixed, and a tile adds
+    // the wave-uniform tile * TR * row_bytes. No clamp: an expert's last tile reads zero
+    // padding rows (in bounds; their outputs are not stored). Held so, the 5-bit kernels spend
+    // one add a copy instead of the clamp and index arithmetic (config 4 gate/up 227 -> 216
+    // us, down 131 -> 125 us). (8-bit full tiles held the same way measured slower: gate/up
+    // 164 -> 178 us on config 3.)
+    uint32_t woff[AQ], tpart[AQ];
 #pragma unroll
-        for (int q = 0; q < AQ; q++) {
-            const int row = (rt0 + ti) * TR + crow[q];
-            woff[q] = (uint32_t)((row < R ? row : R - 1) * (uint32_t)row_bytes) + (uint32_t)coff[q];
+    for (int q = 0; q < AQ; q++)
+        tpart[q] = (uint32_t)(crow[q] >> 7) * (uint32_t)(128 * row_bytes) + (uint32_t)(crow[q] & 127) * (uint32_t)AB +
+                   (uint32_t)coff[q];
+    auto set_tile = [&](int ti) {
+        if constexpr (TL) {
+            const uint32_t tb = (uint32_t)((rt0 + ti) * TR) * (uint32_t)row_bytes;
+#pragma unroll
+            for (int q = 0; q < AQ; q++) woff[q] = tb + tpart[q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < AQ; q++) {
+                const int row0 = (rt0 + ti) * TR + crow[q];
+                const uint32_t row = (uint32_t)(row0 < R ? row0 : R - 1);
+                woff[q] = row * (uint32_t)row_bytes + (uint32_t)coff[q];
+            }
         }
     };
     int iss_ti = 0, iss_kg = 0;
@@ -547,7 +573,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
         // on gfx950 (which kernels failed moved with the schedule; the cause was not found).
         // With the address arithmetic between the copies every build passed the parity tests.
         set_tile(iss_ti);
-        const uint32_t koff = (uint32_t)iss_kg * AB;
+        const uint32_t koff = (uint32_t)iss_kg * KSTEP;
 #pragma unroll
         for (int mm = 0; mm < WMAT; mm++) {
             const int m = mm + mw;
@@ -728,6 +754,31 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     __builtin_amdgcn_s_waitcnt(0);
 }
 
+// One dword of the tile-major 5-bit copy per thread: flattened row f (= expert * rows + row)
+// of [first, first + count), K step kg, dword d of the row's 40-byte piece. Reads walk dev[0]
+// in row-major order.
+__global__ __launch_bounds__(256) void retile5_kernel(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst,
+                                                      size_t first, size_t count, int rows, int G, size_t tile_rows) {
+    const size_t total = count * (size_t)G * 10;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        const size_t f = first + i / ((size_t)G * 10);
+        const int kg = (int)(i / 10 % (size_t)G), d = (int)(i % 10);
+        const size_t e = f / (size_t)rows, row = f % (size_t)rows;
+        const size_t tile = e * (tile_rows / 128) + row / 128;
+        dst[((tile * G + kg) * 128 + row % 128) * 10 + d] = src[f * (size_t)G * 10 + (size_t)kg * 10 + d];
+    }
+}
+
+bool matrix_retile(Matrix *m, size_t first, size_t count, char *error, int capacity) {
+    if (!m->tiled || count == 0) return true;
+    const size_t total = count * m->groups_per_row() * 10;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
+    DIH_LAUNCH(retile5_kernel, dim3(blocks), dim3(256), 0, nullptr, m->packed(), static_cast<uint32_t *>(m->tiled),
+               first, count, m->rows, (int)m->groups_per_row(), m->tiled_rows());
+    return hip_ok(hipGetLastError(), error, capacity, "weight retile") &&
+           hip_ok(hipStreamSynchronize(nullptr), error, capacity, "weight retile");
+}
+
 // Upper bound of (row tile, chunk) work items: sum_g ceil(count_g / BN) <= routes / BN +
 // (groups holding any route); a shared-expert group adds `tokens` routes.
 static size_t qmm_max_work(int rows, int tokens, int ngroups, int dense, int bn, int tile_rows = 128) {
@@ -754,8 +805,9 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         set_error(error, capacity, "Invalid grouped qmm arguments");
         return false;
     }
-    // the streaming kernel addresses an expert's weight rows with 32-bit offsets
-    if ((size_t)m0->rows * ((size_t)m0->columns * m0->bits / 8) > 0x7fffffffu) {
+    // the streaming kernel addresses an expert's weight rows (padded to whole 128-row tiles
+    // in the tile-major copy) with 32-bit offsets
+    if (m0->tiled_rows() * ((size_t)m0->columns * m0->bits / 8) > 0x7fffffffu) {
         set_error(error, capacity, "Matrix too large for one grouped/dense qmm launch");
         return false;
     }
@@ -809,13 +861,27 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         P.rt_groups = (P.row_tiles + rtb - 1) / rtb;
         const size_t lwork = chunks * (size_t)P.rt_groups;
         grid = dim3((unsigned)(8 * ((lwork + 7) / 8)));
+        // 5-bit codes stream from the tile-major copies (every matrix of the launch has one:
+        // same bits and K)
+        if (m0->bits == 5) {
+            const Matrix *ms[4] = {m0, m1, a.sm0, a.sm1};
+            for (const Matrix *mm : ms)
+                if (mm && !mm->tiled) {
+                    set_error(error, capacity, "Missing tile-major 5-bit codes");
+                    return false;
+                }
+            P.p0 = static_cast<const uint32_t *>(m0->tiled);
+            if (m1) P.p1 = static_cast<const uint32_t *>(m1->tiled);
+            if (a.sm0) P.sp0 = static_cast<const uint32_t *>(a.sm0->tiled);
+            if (a.sm1) P.sp1 = static_cast<const uint32_t *>(a.sm1->tiled);
+        }
         // 5-bit gated: the split eight-wave form (gate and up on different waves; its
         // costlier code extraction then overlaps the other wave's MFMAs: 6 % faster on
         // config 4, while 8-bit gated measured no gain)
 #define DIH_QMM_LDS_CASE(B, GT, N, R2)                                              \
         if (m0->bits == B && gated == GT && nt == N && two_slabs == R2) {            \
             constexpr bool SP = GT && B == 5;                                       \
-            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1>), grid, dim3(SP ? 512 : 256), 0, s, P); \
+            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1, B == 5>), grid, dim3(SP ? 512 : 256), 0, s, P); \
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }
         DIH_QMM_LDS_CASE(8, true, 2, false) DIH_QMM_LDS_CASE(8, false, 2, false) DIH_QMM_LDS_CASE(8, false, 4, false)

@@ -5,6 +5,8 @@ Matmul outputs must satisfy max|gpu - oracle| / RMS(oracle) <= TOL (1e-2, the no
 tolerance) against the fp64 oracle of the reference's dequantize-then-matmul; tighter
 bounds are asserted where the arithmetic allows (noted per test).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -511,7 +513,8 @@ def _zipf_logits(rng, T, E, s=1.1):
     (129, 16, 128, 192, 5, "uniform"), (1, 16, 128, 64, 8, "uniform"),
     (96, 64, 1024, 512, 5, "zipf"),    # 5-bit with K multiples of 512: the streaming kernels
     (96, 64, 1024, 512, 8, "zipf"),    # 8-bit streaming gate/up at K=1024 and down at K=512
-    (320, 64, 512, 512, 5, "uniform"), (300, 64, 512, 512, 8, "zipf")])
+    (320, 64, 512, 512, 5, "uniform"), (300, 64, 512, 512, 8, "zipf"),
+    (100, 16, 512, 192, 5, "uniform")])  # 5-bit gate/up of 192 rows: expert codes padded to 256
 def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
     rng = np.random.default_rng(T * 7 + E)
     L = _moe_layer(rng, E, H, I, bits, router=False)
@@ -625,6 +628,66 @@ def test_dense_two_slab_tiles(device, bits, rows, columns, T):
         torch.cuda.synchronize()
         want_bf = orc.dense_f64(host, orc.bf16_bits_to_f32(xb), round_operands=True)
         assert orc.rel_err(y.cpu().numpy(), want_bf) < 1e-4
+    finally:
+        m.dispose()
+
+
+def _device_copy(dst: int, src: int, n: int) -> None:
+    """hipMemcpy through the HIP runtime torch has already loaded (same soname)."""
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(dst, src, n, 4) == 0  # hipMemcpyDefault
+
+
+@pytest.mark.parametrize("path", ["chunks", "staging", "device_ptr"])
+def test_5bit_tile_major_copy_follows_every_write_path(device, path):
+    """5-bit matrices with K a multiple of 512 feed the streaming GEMM from a tile-major copy
+    of their codes, which every write path must keep equal to the row-major codes: direct
+    writes in ragged chunks that start and end inside rows, the host staging buffer, and the
+    device pointer followed by dih_quant_matrix_commit. 200 rows (the copy pads to 256).
+    Rows rewritten after a multiply must reach the next multiply."""
+    L = dh.load()
+    rng = np.random.default_rng(5)
+    rows, columns, T = 200, 512, 130
+    first = orc.random_matrix(rng, 1, rows, columns, 5)
+    second = orc.random_matrix(rng, 1, rows, columns, 5)
+    # the rewrite: rows 37..149 of `second`, the others kept from `first`
+    words = columns * 5 // 32
+    mixed = first.packed.copy().reshape(rows, words)
+    mixed[37:150] = second.packed.reshape(rows, words)[37:150]
+    want_host = orc.QMatrix(mixed, first.scales, first.biases, 1, rows, columns, 5)
+    m = device.allocate(1, rows, columns, 5)
+
+    def put(packed: np.ndarray, lo: int, hi: int) -> None:
+        raw = np.ascontiguousarray(packed).view(np.uint8).reshape(-1)
+        if path == "chunks":
+            cuts = sorted({lo, hi, lo + (hi - lo) // 3 + 7, lo + 2 * (hi - lo) // 3 - 5})
+            for a, b in zip(cuts[:-1], cuts[1:]):
+                m.upload(0, raw[a:b], offset=a)
+        elif path == "staging":
+            m.write(0, raw)
+        else:
+            t = torch.from_numpy(raw[lo:hi].copy()).cuda()
+            torch.cuda.synchronize()
+            _device_copy(m.device_ptr(0) + lo, t.data_ptr(), hi - lo)
+            err = ctypes.create_string_buffer(256)
+            assert L.dih_quant_matrix_commit(m.handle, err, 256) == 0, err.value
+
+    try:
+        row_bytes = words * 4
+        put(first.packed, 0, rows * row_bytes)
+        m.upload(1, first.scales)
+        m.upload(2, first.biases)
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, columns)).astype(np.float32))
+        xf = orc.bf16_bits_to_f32(xb)
+        for host in (first, want_host):
+            if host is want_host:
+                put(mixed, 37 * row_bytes, 150 * row_bytes)
+            y = torch.zeros((T, rows), dtype=torch.float32, device="cuda")
+            dh.dense(device, m, T, dev_bf16(xb), y)
+            torch.cuda.synchronize()
+            want_bf = orc.dense_f64(host, xf, round_operands=True)
+            assert orc.rel_err(y.cpu().numpy(), want_bf) < 1e-4
     finally:
         m.dispose()
 

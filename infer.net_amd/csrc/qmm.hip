@@ -496,14 +496,19 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     // this lane's MFMA row; its scale/bias bf16 bits come eight groups per 16-byte load
     const int r = lane & 31, h = lane >> 5;
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    // The loads go through global-address-space pointers: with the matrix picked by the wave
+    // (split form) the compiler cannot tell the generic pointer is global and emits FLAT
+    // loads, and since a FLAT load may read LDS it first waits for every LDS copy in flight
+    // (a drain of the copy pipeline once per eight steps).
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
     auto win_load = [&](u32x4 (&sw)[RS][2][2], int ti, int w) {
 #pragma unroll
         for (int rs = 0; rs < RS; rs++) {
             const size_t mrow = row_index(rt0 + ti, slab * 32 * RS + 32 * rs + r);
 #pragma unroll
             for (int m = 0; m < WMAT; m++) {
-                sw[rs][m][0] = *reinterpret_cast<const u32x4 *>(psc[m + mw] + mrow * G + 8 * w);
-                sw[rs][m][1] = *reinterpret_cast<const u32x4 *>(pbi[m + mw] + mrow * G + 8 * w);
+                sw[rs][m][0] = *(g_u32x4 *)(psc[m + mw] + mrow * G + 8 * w);
+                sw[rs][m][1] = *(g_u32x4 *)(pbi[m + mw] + mrow * G + 8 * w);
             }
         }
     };

@@ -21,13 +21,15 @@ typedef __attribute__((__vector_size__(2 * sizeof(float)))) float dih_f32x2;
 
 DIH_DEV float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// Round-to-nearest-even f32 -> bf16, two values per v_cvt_pk_bf16_f32 (gfx950). Written
-// as one instruction: from the vector-of-two form the compiler emits one conversion per
-// value plus a v_perm_b32 to merge them.
+// Round-to-nearest-even f32 -> bf16, two values per v_cvt_pk_bf16_f32 (gfx950), through
+// the compiler's vector conversion rather than inline asm: an MFMA that reads a VGPR a VALU
+// instruction has just written needs two wait states, which the compiler inserts only for
+// instructions it can see. (With the conversion in inline asm, some builds placed an MFMA
+// one SALU instruction after it, and that MFMA read the operand's previous contents.)
+typedef __bf16 dih_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float dih_f32v2 __attribute__((ext_vector_type(2)));
 DIH_DEV uint32_t pack_bf16x2(float lo, float hi) {
-    uint32_t r;
-    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
-    return r;
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((dih_f32v2){lo, hi}, dih_bf16x2));
 }
 DIH_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 

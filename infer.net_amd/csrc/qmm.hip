@@ -33,6 +33,8 @@
 // popular expert share that expert's weight rows in the XCD's L2. This replaces the
 // reference's atomic tile list and indirect dispatch (prefill_moe.mm:8-22) with a
 // deterministic order.
+#include <type_traits>
+
 #include "dih_device.h"
 #include "dih_internal.h"
 
@@ -388,22 +390,30 @@ constexpr int qmm_lds_occupancy() {
 // TL: the codes come from the matrix's 128-row tile-major copy (5-bit): a K step of 128 rows
 // is one contiguous 5,120-byte block, so each dword copy instruction of a wave reads 256
 // contiguous bytes instead of pieces of six or seven rows 1,280 bytes apart.
-template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1, bool TL = false>
+// NTC: route tiles multiplied (chunks of 32 * NTC routes) out of the NT tiles' slots the
+// copies fill (slots past NTC tiles repeat the chunk's first route and are not multiplied):
+// 96-route chunks for the 5-bit gated launches of config-4-like routing, where no expert
+// then needs a second chunk.
+template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1, bool TL = false, int NTC = NT>
 __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
-    // 32-route tiles (NT = 1) gave wrong results in the 8-bit grouped down projection, cause
-    // not found (the copy and operand index arithmetic checks out on the host): not built
+    // 32-route tiles (NT = 1) measured slower (config 3 gate/up 181 -> 247 us) and are not
+    // built (their wrong results, like other schedule-dependent failures of this kernel, came
+    // most likely from MFMAs reading bf16 operands converted by inline asm one instruction
+    // earlier; the conversion is now visible to the compiler)
     static_assert(NT >= 2, "route tiles of 64 or more routes only");
     static_assert(!SPLIT || GATED, "only the gated kernel splits its matrices over waves");
     static_assert(RS == 1 || (!GATED && !SPLIT), "two slabs a wave: non-gated only");
     static_assert(!TL || BITS == 5, "tile-major codes: 5-bit only");
     constexpr int TR = 128 * RS;             // rows per row tile
     constexpr int NW = SPLIT ? 8 : 4;        // waves per block
-    constexpr int BN = 32 * NT;
+    static_assert(NTC >= 2 && NTC <= NT, "compute tiles within the copied route slots");
+    constexpr int BN = 32 * NTC;             // routes per chunk (multiplied)
+    constexpr int BC = 32 * NT;              // route slots copied per step (>= BN)
     constexpr int AB = 64 * BITS / 8;        // bytes of one row's codes per K step
     constexpr int A_ST = TR * AB;            // one matrix, one stage
     constexpr int NMAT = GATED ? 2 : 1;
     constexpr int WMAT = SPLIT ? 1 : NMAT;   // matrices one wave dequantizes
-    constexpr int B_ST = BN * 128;
+    constexpr int B_ST = BC * 128;
     constexpr int ST = NMAT * A_ST + B_ST;   // bytes per stage
     constexpr int AQ = (BITS == 8 ? 2 : 5) * RS;   // direct copies per wave per matrix per step
     constexpr int NBW = 4 * NT / NW;         // activation copies (8 routes each) per wave
@@ -417,7 +427,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     __shared__ __align__(16) unsigned char st0[ST], st1[ST], st2[ST], st3[ST];
     // split: silu(gate) of XNT route tiles at a time (in halves when four tiles would not fit
     // beside the stages)
-    constexpr int XNT = SPLIT && NT > 2 ? NT / 2 : NT;
+    constexpr int XNT = SPLIT && NTC > 3 ? NTC / 2 : NTC;
     __shared__ __align__(16) float xch[SPLIT ? 4 * XNT * 16 * 64 : 1];
     lds_escape(st0, st1, st2, st3, xch);
     auto stage_base = [&](int stage) -> unsigned char * {
@@ -497,9 +507,9 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     const int r = lane & 31, h = lane >> 5;
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     // The loads go through global-address-space pointers: with the matrix picked by the wave
-    // (split form) the compiler cannot tell the generic pointer is global and emits FLAT
-    // loads, and since a FLAT load may read LDS it first waits for every LDS copy in flight
-    // (a drain of the copy pipeline once per eight steps).
+    // (split form) the compiler cannot tell the generic pointer is global, emits FLAT loads,
+    // and a FLAT load may read LDS, so it first waits for every LDS copy in flight (a full
+    // drain of the copy pipeline once per eight steps).
     typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
     auto win_load = [&](u32x4 (&sw)[RS][2][2], int ti, int w) {
 #pragma unroll
@@ -524,9 +534,13 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
         bsrc[i] = P.x + (size_t)in_row * C + 8 * (sl ^ ((n >> 1) & 7));
     }
     // output routes of this lane's accumulator columns
-    int out_route[NT];
+    int out_route[NTC];
 #pragma unroll
-    for (int i = 0; i < NT; i++) out_route[i] = route_at(32 * i + r);
+    for (int i = 0; i < NTC; i++) out_route[i] = route_at(32 * i + r);
+    // route tiles holding a valid route (wave-uniform): the main loop is specialized on it, and
+    // the MFMAs and operand reads of the other tiles are skipped (their accumulator columns
+    // are never stored)
+    const int ntu = __builtin_amdgcn_readfirstlane((nvalid + 31) >> 5);
 
     // Copy sources: the expert's first row in each matrix (wave-uniform) plus a 32-bit lane
     // offset of the row within the expert (an expert's rows span less than 2^31 bytes, checked
@@ -573,10 +587,9 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     auto issue = [&](int stage) {
         unsigned char *base = stage_base(stage);
         // The lane offsets are recomputed at every step (a few VALU operations a copy) rather
-        // than held across steps. With them held, the copies issued nearly back to back and,
-        // in some builds, one 32-route activation tile of every chunk never received its data
-        // on gfx950 (which kernels failed moved with the schedule; the cause was not found).
-        // With the address arithmetic between the copies every build passed the parity tests.
+        // than held across steps: the schedule was tuned this way. (Builds that held them
+        // failed parity on one route tile; that failure was most likely the operand hazard of
+        // the former inline-asm bf16 conversion, whose placement moved with the schedule.)
         set_tile(iss_ti);
         const uint32_t koff = (uint32_t)iss_kg * KSTEP;
 #pragma unroll
@@ -606,18 +619,18 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     u32x4 win[RS][2][2], win_next[RS][2][2];
     win_load(win, 0, 0);
 
-    dih_f32x16 acc0[RS][NT], acc1[GATED && !SPLIT ? NT : 1];
+    dih_f32x16 acc0[RS][NTC], acc1[GATED && !SPLIT ? NTC : 1];
     auto zero_acc = [&]() {
 #pragma unroll
         for (int rs = 0; rs < RS; rs++)
 #pragma unroll
-            for (int i = 0; i < NT; i++) {
+            for (int i = 0; i < NTC; i++) {
 #pragma unroll
                 for (int k = 0; k < 16; k++) acc0[rs][i][k] = 0.f;
             }
         if constexpr (GATED && !SPLIT) {
 #pragma unroll
-            for (int i = 0; i < NT; i++) {
+            for (int i = 0; i < NTC; i++) {
 #pragma unroll
                 for (int k = 0; k < 16; k++) acc1[i][k] = 0.f;
             }
@@ -625,6 +638,8 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     };
     zero_acc();
 
+    auto run = [&](auto ntu_c) {
+    constexpr int NTU = decltype(ntu_c)::value;
     for (int ti = 0; ti < nrt; ti++) {
         for (int kw = 0; kw < G; kw += 8) {
             // the next window of scales: this tile's next one, or the next tile's first
@@ -664,14 +679,14 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
                 const unsigned char *bb = base + NMAT * A_ST;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    dih_bf16x8 bx[NT];
+                    dih_bf16x8 bx[NTU];
 #pragma unroll
-                    for (int i = 0; i < NT; i++) {
+                    for (int i = 0; i < NTU; i++) {
                         const int n = 32 * i + r, pc = 4 * h + j;
                         bx[i] = *reinterpret_cast<const dih_bf16x8 *>(bb + n * 128 + 16 * (pc ^ ((n >> 1) & 7)));
                     }
 #pragma unroll
-                    for (int i = 0; i < NT; i++) {
+                    for (int i = 0; i < NTU; i++) {
 #pragma unroll
                         for (int rs = 0; rs < RS; rs++)
                             acc0[rs][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rs * WMAT][j], bx[i], acc0[rs][i], 0, 0, 0);
@@ -693,7 +708,7 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
         // waves of the same slab through LDS (identical lane layouts), XNT route tiles at a
         // time; the up waves store.
 #pragma unroll
-        for (int half = 0; half < NT / XNT; half++) {
+        for (int half = 0; half < NTC / XNT; half++) {
         if constexpr (SPLIT) {
             if (half > 0) {   // the up waves have read the previous half
                 wait_lgkm0();
@@ -754,6 +769,20 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
         }
         }
         zero_acc();
+    }
+    };
+    if constexpr (NTC == 4) {
+        if (ntu >= 4) run(std::integral_constant<int, 4>{});
+        else if (ntu == 3) run(std::integral_constant<int, 3>{});
+        else if (ntu == 2) run(std::integral_constant<int, 2>{});
+        else run(std::integral_constant<int, 1>{});
+    } else if constexpr (NTC == 3) {
+        if (ntu >= 3) run(std::integral_constant<int, 3>{});
+        else if (ntu == 2) run(std::integral_constant<int, 2>{});
+        else run(std::integral_constant<int, 1>{});
+    } else {
+        if (ntu >= 2) run(std::integral_constant<int, 2>{});
+        else run(std::integral_constant<int, 1>{});
     }
     // no copy may still be writing this block's LDS when the block exits
     __builtin_amdgcn_s_waitcnt(0);
@@ -836,7 +865,10 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     // (the grouped down projection keeps 64-route tiles: 96-route tiles, still two blocks a
     // CU, measured 195 -> 209 us on config 4, and 128-route tiles 211 -> 274 us)
     const int nt = streaming && !a.dense && !gated ? 2 : (gated ? (wide_gated ? 4 : 2) : 4);
-    const int bn = 32 * nt;
+    // wide 5-bit gated chunks of 96 routes when experts average at most 64 routes (the copies
+    // still fill 128 route slots; the MFMAs cover 96)
+    const int ntc = wide_gated && (size_t)a.tokens * 8 <= (size_t)64 * (size_t)std::max(1, m0->experts) ? 3 : nt;
+    const int bn = 32 * ntc;
     // dense streaming GEMMs with enough (256-row tile, route chunk) items to fill the GPU:
     // two 32-row slabs per wave (256-row tiles)
     const bool two_slabs = streaming && a.dense && !gated &&
@@ -883,16 +915,16 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         // 5-bit gated: the split eight-wave form (gate and up on different waves; its
         // costlier code extraction then overlaps the other wave's MFMAs: 6 % faster on
         // config 4, while 8-bit gated measured no gain)
-#define DIH_QMM_LDS_CASE(B, GT, N, R2)                                              \
-        if (m0->bits == B && gated == GT && nt == N && two_slabs == R2) {            \
+#define DIH_QMM_LDS_CASE(B, GT, N, R2, NC)                                          \
+        if (m0->bits == B && gated == GT && nt == N && two_slabs == R2 && ntc == NC) { \
             constexpr bool SP = GT && B == 5;                                       \
-            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1, B == 5>), grid, dim3(SP ? 512 : 256), 0, s, P); \
+            DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1, B == 5, NC>), grid, dim3(SP ? 512 : 256), 0, s, P); \
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }
-        DIH_QMM_LDS_CASE(8, true, 2, false) DIH_QMM_LDS_CASE(8, false, 2, false) DIH_QMM_LDS_CASE(8, false, 4, false)
-        DIH_QMM_LDS_CASE(5, true, 2, false) DIH_QMM_LDS_CASE(5, false, 2, false) DIH_QMM_LDS_CASE(5, false, 4, false)
-        DIH_QMM_LDS_CASE(5, true, 4, false)
-        DIH_QMM_LDS_CASE(8, false, 4, true) DIH_QMM_LDS_CASE(5, false, 4, true)
+        DIH_QMM_LDS_CASE(8, true, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 4, false, 4)
+        DIH_QMM_LDS_CASE(5, true, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 4, false, 4)
+        DIH_QMM_LDS_CASE(5, true, 4, false, 4) DIH_QMM_LDS_CASE(5, true, 4, false, 3)
+        DIH_QMM_LDS_CASE(8, false, 4, true, 4) DIH_QMM_LDS_CASE(5, false, 4, true, 4)
 #undef DIH_QMM_LDS_CASE
     }
 #define DIH_QMM_CASE(B, GT, N, D)                                                   \

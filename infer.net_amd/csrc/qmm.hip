@@ -889,10 +889,12 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         const size_t chunks = work / (size_t)P.row_tiles;
         const size_t per_tile = (size_t)P.row_tiles * chunks;
         int rtb = (int)std::min<size_t>(4, std::max<size_t>(1, per_tile / 512));
-        // 5-bit gated (one eight-wave block per CU): single row tiles. Its work items are
-        // nearly equal, and with four tiles a block the last round of blocks ran almost
-        // empty (config 4 gate/up 457 -> 380 us; 8-bit gated measured best as above)
-        if (gated && m0->bits == 5) rtb = 1;
+        // Gated launches (one block per CU): single row tiles. 5-bit: its work items are
+        // nearly equal, and with four tiles a block the last round of blocks ran almost empty
+        // (config 4 gate/up 457 -> 380 us). 8-bit: since the MFMAs of empty route tiles are
+        // skipped, single tiles measured faster too (config 3 gate/up 166 -> 154 us); the
+        // non-gated down projection keeps up to four (single tiles: 89 -> 101 us)
+        if (gated) rtb = 1;
         rtb = std::min(rtb, P.row_tiles);
         P.rtb = rtb;
         P.rt_groups = (P.row_tiles + rtb - 1) / rtb;

@@ -371,12 +371,13 @@ __global__ __launch_bounds__(256, 2) void qmm_kernel(QmmParams P) {
 
 // (to_lds, wait_vm, wait_lgkm0 and barrier_no_fence are in dih_device.h)
 
-// Blocks per CU the streaming kernel is built for: two for the narrow route tiles (32 rows
-// of accumulators per matrix) when four stages fit in half the LDS; the VGPR budget is then
-// 256 per lane, accumulators included. The split gated form (eight waves) runs one block.
+// Blocks per CU the streaming kernel is built for: two for the narrow route tiles (two
+// 32-route tiles per matrix, three for one 5-bit matrix) when four stages fit in half the
+// LDS; the VGPR budget is then 256 per lane, accumulators included. The split gated form
+// (eight waves) runs one block.
 template <int BITS, bool GATED, int NT, bool SPLIT>
 constexpr int qmm_lds_occupancy() {
-    return !SPLIT && (GATED ? 2 : 1) * NT <= 2 &&
+    return !SPLIT && (GATED ? 2 : 1) * NT <= (BITS == 5 ? 3 : 2) &&
                    4 * ((GATED ? 2 : 1) * 128 * (64 * BITS / 8) + 32 * NT * 128) <= 80 * 1024
                ? 2 : 1;
 }
@@ -862,9 +863,13 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     // twice (config 4: 64 routes on average, at most ~90)
     const bool wide_gated = streaming && gated && !a.dense && m0->bits == 5 &&
                             (size_t)a.tokens * 8 > (size_t)48 * (size_t)std::max(1, m0->experts);
-    // (the grouped down projection keeps 64-route tiles: 96-route tiles, still two blocks a
-    // CU, measured 195 -> 209 us on config 4, and 128-route tiles 211 -> 274 us)
-    const int nt = streaming && !a.dense && !gated ? 2 : (gated ? (wide_gated ? 4 : 2) : 4);
+    // The grouped 5-bit down projection takes 96-route tiles (still two blocks a CU) when
+    // experts average more than 48 routes: config 4's experts (at most ~90 routes) then need
+    // one chunk each (down 126 -> 119 us; 128-route tiles, one block a CU, measured 211 ->
+    // 274 us). Other grouped down projections keep 64-route tiles.
+    const bool wide_down = streaming && !gated && !a.dense && m0->bits == 5 &&
+                           (size_t)a.tokens * 8 > (size_t)48 * (size_t)std::max(1, m0->experts);
+    const int nt = streaming && !a.dense && !gated ? (wide_down ? 3 : 2) : (gated ? (wide_gated ? 4 : 2) : 4);
     // wide 5-bit gated chunks of 96 routes when experts average at most 64 routes (the copies
     // still fill 128 route slots; the MFMAs cover 96)
     const int ntc = wide_gated && (size_t)a.tokens * 8 <= (size_t)64 * (size_t)std::max(1, m0->experts) ? 3 : nt;
@@ -924,7 +929,7 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }
         DIH_QMM_LDS_CASE(8, true, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 4, false, 4)
-        DIH_QMM_LDS_CASE(5, true, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 4, false, 4)
+        DIH_QMM_LDS_CASE(5, true, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 3, false, 3) DIH_QMM_LDS_CASE(5, false, 4, false, 4)
         DIH_QMM_LDS_CASE(5, true, 4, false, 4) DIH_QMM_LDS_CASE(5, true, 4, false, 3)
         DIH_QMM_LDS_CASE(8, false, 4, true, 4) DIH_QMM_LDS_CASE(5, false, 4, true, 4)
 #undef DIH_QMM_LDS_CASE

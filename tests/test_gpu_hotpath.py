@@ -515,7 +515,8 @@ def _zipf_logits(rng, T, E, s=1.1):
     (96, 64, 1024, 512, 8, "zipf"),    # 8-bit streaming gate/up at K=1024 and down at K=512
     (320, 64, 512, 512, 5, "uniform"), (300, 64, 512, 512, 8, "zipf"),
     (100, 16, 512, 192, 5, "uniform"),  # 5-bit gate/up of 192 rows: expert codes padded to 256
-    (120, 16, 512, 256, 5, "zipf")])     # 5-bit split gated, 128-route chunks, popular experts split
+    (120, 16, 512, 256, 5, "zipf"),      # 5-bit split gated, 96-route chunks, popular experts split
+    (100, 16, 512, 512, 5, "zipf")])     # 5-bit down in 96-route tiles (experts average 50 routes)
 def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
     rng = np.random.default_rng(T * 7 + E)
     L = _moe_layer(rng, E, H, I, bits, router=False)

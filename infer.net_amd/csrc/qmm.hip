@@ -919,12 +919,12 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
             if (a.sm0) P.sp0 = static_cast<const uint32_t *>(a.sm0->tiled);
             if (a.sm1) P.sp1 = static_cast<const uint32_t *>(a.sm1->tiled);
         }
-        // 5-bit gated: the split eight-wave form (gate and up on different waves; its
-        // costlier code extraction then overlaps the other wave's MFMAs: 6 % faster on
-        // config 4, while 8-bit gated measured no gain)
+        // Gated launches: the split eight-wave form (gate and up on different waves, so one
+        // wave's dequant overlaps the other's MFMAs and waits): 6 % faster on config 4, and,
+        // since empty route tiles are skipped, config 3 gate/up 154 -> 143 us
 #define DIH_QMM_LDS_CASE(B, GT, N, R2, NC)                                          \
         if (m0->bits == B && gated == GT && nt == N && two_slabs == R2 && ntc == NC) { \
-            constexpr bool SP = GT && B == 5;                                       \
+            constexpr bool SP = GT;                                                 \
             DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1, B == 5, NC>), grid, dim3(SP ? 512 : 256), 0, s, P); \
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }

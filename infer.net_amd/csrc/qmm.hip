@@ -397,17 +397,17 @@ constexpr int qmm_lds_occupancy() {
 // then needs a second chunk.
 template <int BITS, bool GATED, int NT, int S, bool SPLIT, int RS = 1, bool TL = false, int NTC = NT>
 __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<BITS, GATED, NT, SPLIT>())) void qmm_lds_kernel(QmmParams P) {
-    // 32-route tiles (NT = 1) measured slower (config 3 gate/up 181 -> 247 us) and are not
-    // built (their wrong results, like other schedule-dependent failures of this kernel, came
-    // most likely from MFMAs reading bf16 operands converted by inline asm one instruction
-    // earlier; the conversion is now visible to the compiler)
-    static_assert(NT >= 2, "route tiles of 64 or more routes only");
+    // 32-route tiles (NT = 1) serve the 8-bit grouped down projection of sparse routing only
+    // (gate/up measured slower: config 3 181 -> 247 us). Their earlier wrong results, like
+    // other schedule-dependent failures of this kernel, came from MFMAs reading bf16 operands
+    // converted by inline asm one instruction earlier; the conversion is now visible to the
+    // compiler.
     static_assert(!SPLIT || GATED, "only the gated kernel splits its matrices over waves");
     static_assert(RS == 1 || (!GATED && !SPLIT), "two slabs a wave: non-gated only");
     static_assert(!TL || BITS == 5, "tile-major codes: 5-bit only");
     constexpr int TR = 128 * RS;             // rows per row tile
     constexpr int NW = SPLIT ? 8 : 4;        // waves per block
-    static_assert(NTC >= 2 && NTC <= NT, "compute tiles within the copied route slots");
+    static_assert(NTC >= 1 && NTC <= NT, "compute tiles within the copied route slots");
     constexpr int BN = 32 * NTC;             // routes per chunk (multiplied)
     constexpr int BC = 32 * NT;              // route slots copied per step (>= BN)
     constexpr int AB = 64 * BITS / 8;        // bytes of one row's codes per K step
@@ -781,9 +781,11 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
         if (ntu >= 3) run(std::integral_constant<int, 3>{});
         else if (ntu == 2) run(std::integral_constant<int, 2>{});
         else run(std::integral_constant<int, 1>{});
-    } else {
+    } else if constexpr (NTC == 2) {
         if (ntu >= 2) run(std::integral_constant<int, 2>{});
         else run(std::integral_constant<int, 1>{});
+    } else {
+        run(std::integral_constant<int, 1>{});
     }
     // no copy may still be writing this block's LDS when the block exits
     __builtin_amdgcn_s_waitcnt(0);
@@ -866,10 +868,14 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     // The grouped 5-bit down projection takes 96-route tiles (still two blocks a CU) when
     // experts average more than 48 routes: config 4's experts (at most ~90 routes) then need
     // one chunk each (down 126 -> 119 us; 128-route tiles, one block a CU, measured 211 ->
-    // 274 us). Other grouped down projections keep 64-route tiles.
+    // 274 us). The 8-bit one takes 32-route tiles (three blocks a CU) when experts average
+    // at most 16 routes (config 3 down 88.7 -> 86.2 us). Others keep 64-route tiles.
     const bool wide_down = streaming && !gated && !a.dense && m0->bits == 5 &&
                            (size_t)a.tokens * 8 > (size_t)48 * (size_t)std::max(1, m0->experts);
-    const int nt = streaming && !a.dense && !gated ? (wide_down ? 3 : 2) : (gated ? (wide_gated ? 4 : 2) : 4);
+    const bool narrow_down = streaming && !gated && !a.dense && m0->bits == 8 &&
+                             (size_t)a.tokens * 8 <= (size_t)16 * (size_t)std::max(1, m0->experts);
+    const int nt = streaming && !a.dense && !gated ? (wide_down ? 3 : narrow_down ? 1 : 2)
+                                                   : (gated ? (wide_gated ? 4 : 2) : 4);
     // wide 5-bit gated chunks of 96 routes when experts average at most 64 routes (the copies
     // still fill 128 route slots; the MFMAs cover 96)
     const int ntc = wide_gated && (size_t)a.tokens * 8 <= (size_t)64 * (size_t)std::max(1, m0->experts) ? 3 : nt;
@@ -928,7 +934,7 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
             DIH_LAUNCH((qmm_lds_kernel<B, GT, N, 4, SP, R2 ? 2 : 1, B == 5, NC>), grid, dim3(SP ? 512 : 256), 0, s, P); \
             return hip_ok(hipGetLastError(), error, capacity, "qmm launch");        \
         }
-        DIH_QMM_LDS_CASE(8, true, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 4, false, 4)
+        DIH_QMM_LDS_CASE(8, true, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 2, false, 2) DIH_QMM_LDS_CASE(8, false, 1, false, 1) DIH_QMM_LDS_CASE(8, false, 4, false, 4)
         DIH_QMM_LDS_CASE(5, true, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 2, false, 2) DIH_QMM_LDS_CASE(5, false, 3, false, 3) DIH_QMM_LDS_CASE(5, false, 4, false, 4)
         DIH_QMM_LDS_CASE(5, true, 4, false, 4) DIH_QMM_LDS_CASE(5, true, 4, false, 3)
         DIH_QMM_LDS_CASE(8, false, 4, true, 4) DIH_QMM_LDS_CASE(5, false, 4, true, 4)

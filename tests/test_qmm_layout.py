@@ -10,8 +10,8 @@ then checks what the kernel relies on:
 * and it is the byte the MFMA needs: weight row `wr`, codes 32h + 8j .. +7 of the K step
   for MFMA j in lane half h, and route slot n's activations 32h + 8j .. +7 likewise;
 * the epilogue's accumulator layout covers each (row, route slot) of the tile exactly once.
-NT = 1 (32-route tiles, not built: `static_assert(NT >= 2)`) is checked as well; its index
-arithmetic is as consistent as the built widths'.
+NT = 1 (32-route tiles, built for the 8-bit grouped down projection of sparse routing) is
+checked as well.
 """
 import itertools
 

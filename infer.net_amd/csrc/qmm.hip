@@ -856,10 +856,11 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     // Route tile width: 64 routes for the gated kernels, 128 otherwise (the register-ring
     // kernel measured faster so than with narrower tiles and deeper rings). Grouped
     // non-gated streaming launches (K a multiple of 512) use 64: experts average a few
-    // routes, and the narrower tile lets two blocks share a CU.
+    // routes, and the narrower tile lets two blocks share a CU. Exceptions by the routes
+    // per expert follow.
     const bool gated = m1 != nullptr;
     const bool streaming = m0->columns % 512 == 0;
-    // 5-bit gated (the split eight-wave form) takes 128-route tiles when experts average
+    // 5-bit gated takes 128 route slots when experts average
     // more than 48 routes (uniform routing over E experts: 8T/E): 64-route tiles would give
     // an expert of 65-127 routes a second, mostly empty chunk and dequantize its weights
     // twice (config 4: 64 routes on average, at most ~90)

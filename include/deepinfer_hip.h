@@ -272,12 +272,10 @@ int dih_grouped_qmm(void *context, void *matrix, void *up_matrix, int tokens, co
 
 /* Dense batched projection (p_gemv dense path, gpu_prefill.mm:603-620, prefill_bf16.mm:7-53):
  * Y[t][r] = sum_c w(0,r,c)*X[t][c]. Up to 4 tokens: a batched f32 GEMV; up to 1023 tokens
- * (511 for matrices above 4096 rows): the fused MFMA qmm with bf16 operands; longer chunks:
- * the matrix dequantized once into bf16 context scratch (2*R*C bytes), then a hipBLASLt bf16
- * GEMM. bf16 operands, f32 accumulation in both MFMA forms. x bf16 [T][C]; y f32 or bf16
- * [T][R]. The first long chunk of each (R, C, T, y type) picks and caches a GEMM algorithm
- * by timing the heuristic's candidates on `stream` (synchronizing it), unless the stream is
- * being captured. */
+ * (511 for matrices of up to 4096 rows): the fused MFMA qmm with bf16 operands; longer
+ * chunks: the matrix dequantized once into bf16 context scratch (2*R*C bytes), then the
+ * library's bf16 MFMA GEMM. bf16 operands, f32 accumulation in every MFMA form. x bf16
+ * [T][C]; y f32 or bf16 [T][R]. */
 int dih_dense(void *context, void *matrix, int tokens, const void *x, void *y, int y_dtype,
               void *stream, char *error, int capacity);
 

@@ -232,7 +232,6 @@ __attribute__((visibility("default"))) void dih_quant_destroy(void *p) {
     Context *c = as_ctx(p);
     if (!c) return;
     (void)hipStreamSynchronize(c->stream);
-    blas_release(c);
     for (auto &s : c->ws)
         if (s.ptr) (void)hipFree(s.ptr);
     for (auto &e : c->prof_pool) (void)hipEventDestroy(e);
@@ -1077,15 +1076,12 @@ __attribute__((visibility("default"))) int dih_dense(void *ctx, void *matrix, in
     // Dispatch policy (p_gemv, gpu_prefill.mm:603-620, picks GEMV kernels below 64 tokens):
     // up to kDenseGemvTokens tokens run as one batched GEMV launch (each token a slot of
     // expert 0; measured 8 / 13 / 18 us against 26 us for the MFMA tile at 1 / 2 / 4 tokens
-    // of an 8192 x 2048 8-bit matrix), long chunks as a bf16 GEMM after one dequantization
+    // of an 8192 x 2048 8-bit matrix), long chunks as the bf16 GEMM after one dequantization
     // pass (the fused tile re-dequantizes the weights for every 128 tokens), the rest as the
-    // fused MFMA GEMM. Measured for the config-5 matrices: at 1024 tokens and more the bf16
-    // GEMM wins for every shape (8192 x 2048: 54 us either way at 1024, 126 vs 185 us at
-    // 4096); at 512 it wins up to 4096 rows (512 x 2048: 15 vs 24 us; 2048 x 4096: 33 vs
-    // 45 us) while the fused tile keeps taller matrices (8192 x 2048: 32 vs 44 us).
+    // fused MFMA GEMM.
     constexpr int kDenseGemvTokens = 4;
     if (tokens >= 1024 || (tokens >= 512 && m->rows <= 4096)) {
-        bool ok = launch_dense_blas(c, m, tokens, static_cast<const uint16_t *>(x), y, y_dtype == DIH_BF16, s,
+        bool ok = launch_dense_gemm(c, m, tokens, static_cast<const uint16_t *>(x), y, y_dtype == DIH_BF16, s,
                                     error, capacity);
         prof_mark(c, s, "dense_qmm");
         return ok ? 0 : -1;

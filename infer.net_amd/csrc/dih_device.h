@@ -305,3 +305,13 @@ template <typename T>
 DIH_DEV void lds_escape_one(T *p) { asm volatile("" ::"r"(p) : "memory"); }
 template <typename... P>
 DIH_DEV void lds_escape(P... p) { (lds_escape_one(p), ...); }
+
+// Logical work item of physical block b when `items` items run on a grid sized for an
+// upper bound of them: L = (b % 8) * per + b / 8 with per = ceil(items / 8), so that
+// consecutive items share an XCD (and its L2) and the actual items, not the bound, are
+// spread over all eight XCDs. -1 for a block with no item.
+DIH_DEV int xcd_item(int b, int items) {
+    const int per = (items + 7) >> 3;
+    const int L = (b & 7) * per + (b >> 3);
+    return (b >> 3) < per && L < items ? L : -1;
+}

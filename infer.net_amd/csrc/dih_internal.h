@@ -26,7 +26,7 @@ struct Matrix {
     size_t stage_in_bytes = 0, stage_out_bytes = 0;
     // 5-bit matrices with K a multiple of 512: a second copy of the codes in 128-row
     // tile-major order, [expert][row tile][K step][row in tile][40 bytes], rows padded to
-    // a multiple of 128 with zeros, read by the streaming grouped/dense GEMM (one K step of
+    // a multiple of 256 with zeros, read by the streaming grouped/dense GEMM (one K step of
     // a row tile is then 5,120 contiguous bytes instead of 128 40-byte pieces 1,280 bytes
     // apart). Kept equal to dev[0] by every write path (matrix_retile).
     void *tiled = nullptr;
@@ -38,7 +38,9 @@ struct Matrix {
     const uint16_t *biases() const { return static_cast<const uint16_t *>(dev[2]); }
     size_t words_per_row() const { return (size_t)columns * bits / 32; }
     size_t groups_per_row() const { return (size_t)columns / 64; }
-    size_t tiled_rows() const { return ((size_t)rows + 127) / 128 * 128; }  // per expert
+    // per expert: whole 256-row tiles, so that the dense two-slab tiles (256 rows) read
+    // padding, not past the copy
+    size_t tiled_rows() const { return ((size_t)rows + 255) / 256 * 256; }
 };
 
 // Grow-only device scratch buffer.
@@ -66,16 +68,13 @@ struct Context {
     // address, looked up once per device), or null with the lookup's error
     void *noalloc = nullptr;
     std::string noalloc_error;
-    // hipBLASLt handle and the dense projections' GEMM plans (dense_blas.hip), created on
-    // first use
-    void *blas = nullptr;
     uint32_t magic = 0x44494358u;
 };
 
 enum ScratchId {
     S_IDS, S_PROBS, S_STATUS, S_LOGITS, S_SROUTE, S_SACT, S_ACT, S_SOUT,
     S_COUNTS, S_ROUTES, S_CHUNKS, S_NCHUNKS, S_ACTBF, S_ROUTEOUT, S_ARGVAL, S_ARGIDX,
-    S_STAGE_X, S_STAGE_Y, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_W16, S_BLASWS, S_COUNT_
+    S_STAGE_X, S_STAGE_Y, S_APART, S_ASTAT, S_DW, S_DU, S_DQ, S_DCU, S_DF, S_ASCORE, S_W16, S_COUNT_
 };
 static_assert(S_COUNT_ <= (int)(sizeof(Context::ws) / sizeof(Scratch)), "scratch table too small");
 
@@ -243,12 +242,14 @@ int attention_partials(int position, int tokens, int partition);
 // Floats of score scratch the decode scores pass needs (0: none).
 size_t attention_score_floats(int position, int tokens, int round, int partition);
 
-// Dense projection of a long chunk: matrix dequantized into bf16 scratch, then a hipBLASLt
-// bf16 GEMM with f32 accumulation (dense_blas.hip). blas_release frees the context's
-// hipBLASLt state.
-bool launch_dense_blas(Context *c, const Matrix *m, int tokens, const uint16_t *x, void *y, bool y_bf16,
+// Dense projection of a long chunk (gemm.hip): the matrix dequantized into bf16 scratch,
+// then the library's bf16 MFMA GEMM with f32 accumulation, Y[T][R] = X[T][C] * W16[R][C]^T.
+bool launch_dense_gemm(Context *c, const Matrix *m, int tokens, const uint16_t *x, void *y, bool y_bf16,
                        hipStream_t s, char *error, int capacity);
-void blas_release(Context *c);
+bool launch_gemm_bf16(const uint16_t *w16, int R, int C, int tokens, const uint16_t *x, void *y, bool y_bf16,
+                      hipStream_t s, char *error, int capacity);
+bool launch_dequant_bf16_rows(const uint32_t *packed, const uint16_t *scales, const uint16_t *biases, int bits,
+                              int rows, int columns, uint16_t *out, hipStream_t s, char *error, int capacity);
 bool launch_attention(const AttentionArgs &a, hipStream_t s, char *error, int capacity);
 
 // Gated delta rule over a chunk (delta.hip): state [32][128][128] f32 and history

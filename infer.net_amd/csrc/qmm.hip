@@ -123,16 +123,6 @@ DIH_DEV int chunk_total(const uint32_t *counts, int ngroups) {
     return run;
 }
 
-// Logical work item of physical block b when `items` items run on a grid sized for an
-// upper bound of them: L = (b % 8) * per + b / 8 with per = ceil(items / 8), so that
-// consecutive items share an XCD (and its L2) and the actual items, not the bound, are
-// spread over all eight XCDs. -1 for a block with no item.
-DIH_DEV int xcd_item(int b, int items) {
-    const int per = (items + 7) >> 3;
-    const int L = (b & 7) * per + (b >> 3);
-    return (b >> 3) < per && L < items ? L : -1;
-}
-
 // The MFMAs of one 64-column K step over the first NTU route tiles; each 16-column slice's
 // B operands are read from LDS before its MFMAs so the reads overlap.
 template <bool GATED, int NTU, int NT>
@@ -547,12 +537,12 @@ __global__ __launch_bounds__(SPLIT ? 512 : 256, (RS > 1 ? 1 : qmm_lds_occupancy<
     // offset of the row within the expert (an expert's rows span less than 2^31 bytes, checked
     // on the host); a K step adds the wave-uniform offset kg * KSTEP. Row-major codes: a row
     // starts row * row_bytes in, a K step is AB bytes further. Tile-major codes (experts padded
-    // to whole 128-row tiles): a 128-row tile starts tile * 128 * row_bytes in, its row rr
+    // to whole 256-row tiles, so a 256-row dense tile stays inside the copy): a 128-row tile starts tile * 128 * row_bytes in, its row rr
     // rr * AB further, and a K step is 128 * AB bytes. The issue position (the next step to
     // copy, as tile and K step) is wave-uniform, so the step bookkeeping is scalar and no step
     // index is divided at run time.
     constexpr uint32_t KSTEP = TL ? 128 * AB : AB;
-    const size_t wrows = TL ? (size_t)((R + 127) & ~127) : (size_t)R;  // code rows per expert
+    const size_t wrows = TL ? (size_t)((R + 255) & ~255) : (size_t)R;  // code rows per expert
     const char *wbase[WMAT];
 #pragma unroll
     for (int mm = 0; mm < WMAT; mm++) wbase[mm] = pw[mm + mw] + (size_t)(shared ? 0 : e) * wrows * row_bytes;
@@ -842,7 +832,7 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
         set_error(error, capacity, "Invalid grouped qmm arguments");
         return false;
     }
-    // the streaming kernel addresses an expert's weight rows (padded to whole 128-row tiles
+    // the streaming kernel addresses an expert's weight rows (padded to whole 256-row tiles
     // in the tile-major copy) with 32-bit offsets
     if (m0->tiled_rows() * ((size_t)m0->columns * m0->bits / 8) > 0x7fffffffu) {
         set_error(error, capacity, "Matrix too large for one grouped/dense qmm launch");

@@ -588,42 +588,6 @@ bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t 
     return false;
 }
 
-// Full-matrix dequantization to bf16 (expanded_weights, prefill_bf16_expanded.mm:8-16):
-// one thread per 32-code chunk.
-template <int BITS>
-__global__ void dequant_bf16_kernel(const uint32_t *packed, const uint16_t *scales,
-                                    const uint16_t *biases, int rows, int columns, uint16_t *out) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int nchunk = columns >> 5;
-    if (i >= (size_t)rows * nchunk) return;
-    const size_t r = i / nchunk;
-    const int ch = (int)(i - r * nchunk);
-    Chunk<BITS> c;
-    load_chunk<BITS>(c, packed + r * ((size_t)columns * BITS / 32), ch);
-    float s = bf16_to_f32(scales[r * (columns >> 6) + (ch >> 1)]);
-    float b = bf16_to_f32(biases[r * (columns >> 6) + (ch >> 1)]);
-    dih_bf16x8 op[4];
-    chunk_to_bf16<BITS>(c, s, b, op);
-    uint4 *o = reinterpret_cast<uint4 *>(out + r * columns + (size_t)ch * 32);
-#pragma unroll
-    for (int q = 0; q < 4; q++) o[q] = __builtin_bit_cast(uint4, op[q]);
-}
-
-bool launch_dequant_bf16(const Matrix *m, int expert, uint16_t *out, hipStream_t s, char *error,
-                         int capacity) {
-    const size_t off = (size_t)expert * m->rows;
-    const size_t n = (size_t)m->rows * (m->columns / 32);
-    dim3 grid((unsigned)((n + 255) / 256)), block(256);
-    const uint32_t *p = m->packed() + off * m->words_per_row();
-    const uint16_t *sc = m->scales() + off * m->groups_per_row();
-    const uint16_t *bi = m->biases() + off * m->groups_per_row();
-    if (m->bits == 8)
-        DIH_LAUNCH((dequant_bf16_kernel<8>), grid, block, 0, s, p, sc, bi, m->rows, m->columns, out);
-    else
-        DIH_LAUNCH((dequant_bf16_kernel<5>), grid, block, 0, s, p, sc, bi, m->rows, m->columns, out);
-    return hip_ok(hipGetLastError(), error, capacity, "dequant launch");
-}
-
 // One row to f32 (di_quant_embedding quantized.mm:384-397 / graph_embedding
 // gpu_graph.mm:22-31): one thread per column.
 __global__ void embedding_kernel(const uint32_t *packed, const uint16_t *scales,

@@ -226,13 +226,15 @@ def test_config4_prefill_2048_tokens_5bit_uniform(device):
 
 # ------------------------------------------------------------------------- config 5
 
-@pytest.mark.parametrize("name,rows,cols", [("q_gate", 8192, 2048), ("k", 512, 2048), ("v", 512, 2048),
-                                            ("o", 2048, 4096), ("in_proj", 12288, 2048)])
-def test_config5_dense_4096_tokens(device, name, rows, cols):
-    """Each config-5 projection at a 4096-token chunk: within 1e-4 of the fp64 product of
-    bf16-rounded operands (the reference's BF16 GEMM), within TOL of the unrounded one;
-    the bf16 output is one RNE step from the f32 output's answer."""
-    T = 4096
+@pytest.mark.parametrize("name,rows,cols,T", [("q_gate", 8192, 2048, 4096), ("k", 512, 2048, 4096),
+                                              ("v", 512, 2048, 4096), ("o", 2048, 4096, 4096),
+                                              ("in_proj", 12288, 2048, 4096), ("q_gate", 8192, 2048, 2048),
+                                              ("o", 2048, 4096, 2048)])
+def test_config5_dense_4096_tokens(device, name, rows, cols, T):
+    """Each config-5 projection at a 4096-token chunk (and the reference's default 2048-token
+    prefill chunk): within 1e-4 of the fp64 product of bf16-rounded operands (the reference's
+    BF16 GEMM), within TOL of the unrounded one; the bf16 output is one RNE step from the
+    f32 output's answer."""
     rng = np.random.default_rng(rows + cols)
     host = orc.random_matrix(rng, 1, rows, cols, 8)
     m = upload(device, host)

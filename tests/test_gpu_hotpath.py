@@ -516,7 +516,8 @@ def _zipf_logits(rng, T, E, s=1.1):
     (320, 64, 512, 512, 5, "uniform"), (300, 64, 512, 512, 8, "zipf"),
     (100, 16, 512, 192, 5, "uniform"),  # 5-bit gate/up of 192 rows: expert codes padded to 256
     (120, 16, 512, 256, 5, "zipf"),      # 5-bit split gated, 96-route chunks, popular experts split
-    (100, 16, 512, 512, 5, "zipf")])     # 5-bit down in 96-route tiles (experts average 50 routes)
+    (100, 16, 512, 512, 5, "zipf"),      # 5-bit down in 96-route tiles (experts average 50 routes)
+    (200, 16, 512, 256, 5, "uniform")])  # 5-bit split gated in 128-route chunks (experts average 100)
 def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
     rng = np.random.default_rng(T * 7 + E)
     L = _moe_layer(rng, E, H, I, bits, router=False)

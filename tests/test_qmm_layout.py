@@ -151,44 +151,63 @@ def test_epilogue_covers_each_output_once(nt):
     assert len(seen) == 128 * 32 * nt
 
 
-@pytest.mark.parametrize("rows,rs", [(256, 1), (200, 1), (384, 2), (300, 2)])
+def _tile_major_offsets(rows, rs, experts, G):
+    """Byte offsets (into the tile-major copy) of every 4-byte piece the streaming kernel's
+    copies read, padding rows included, and the (expert, row, piece offset, K step) each
+    one belongs to. The copy pads an expert's rows to whole 256-row tiles (Matrix::tiled_rows);
+    a copy lane's offset is tile * TR * row_bytes + (crow >> 7) * 128 * row_bytes +
+    (crow & 127) * 40 + its piece offset, plus 128 * 40 per K step (qmm_lds_kernel)."""
+    import numpy as np
+    ab, row_bytes = 40, 40 * G
+    rows_pad = (rows + 255) // 256 * 256
+    tr = 128 * rs
+    e, rt, slab, q, lane, kg = np.meshgrid(np.arange(experts), np.arange((rows + tr - 1) // tr), np.arange(4),
+                                           np.arange(5 * rs), np.arange(64), np.arange(G), indexing="ij")
+    i = 64 * q + lane
+    rl = i // 10
+    crow, coff = slab * 32 * rs + rl, 4 * (i - rl * 10)
+    row = rt * tr + crow
+    tpart = (crow >> 7) * 128 * row_bytes + (crow & 127) * ab + coff
+    t_off = e * rows_pad * row_bytes + rt * tr * row_bytes + tpart + kg * 128 * ab
+    return t_off, e, row, coff, kg, rows_pad
+
+
+@pytest.mark.parametrize("rows,rs", [(256, 1), (200, 1), (384, 2), (300, 2), (129, 2)])
 def test_tile_major_reads_match_row_major(rows, rs):
     """5-bit streaming launches read the codes from the tile-major copy that
     retile5_kernel writes ([expert][row tile][K step][row in tile][40 bytes], rows padded to
-    whole 128-row tiles): a copy lane's offset there is tile * 128 * row_bytes +
-    (row >> 7 within the tile) * 128 * row_bytes + (row & 127) * 40 + its piece offset, plus
-    128 * 40 per K step. Restates both index maps (the kernel's and the retile kernel's) on
+    whole 256-row tiles). Restates both index maps (the kernel's and the retile kernel's) on
     two experts and checks every byte a copy reads is the byte the row-major layout holds
-    at row * row_bytes + K step * 40 + piece offset (rows past the matrix are clamped in the
-    row-major layout and padding in the tile-major one; neither is stored)."""
+    at row * row_bytes + K step * 40 + piece offset, for rows of the matrix, and zero
+    padding inside the copy for the rows past it (their outputs are not stored)."""
     import numpy as np
     experts, G = 2, 8
-    ab, row_bytes = 40, 40 * G
-    rows_pad = (rows + 127) // 128 * 128
+    row_bytes = 40 * G
+    t_off, e, row, coff, kg, rows_pad = _tile_major_offsets(rows, rs, experts, G)
     packed = np.arange(experts * rows * row_bytes, dtype=np.int64)   # byte b holds b
     words = packed.reshape(experts * rows, G, 10, 4)
     tiled = np.full(experts * rows_pad * row_bytes, -1, dtype=np.int64)
     for f in range(experts * rows):                                   # retile5_kernel
-        e, row = divmod(f, rows)
-        tile = e * (rows_pad // 128) + row // 128
-        for kg in range(G):
+        ee, rr = divmod(f, rows)
+        tile = ee * (rows_pad // 128) + rr // 128
+        for k in range(G):
             for d in range(10):
-                dst = ((tile * G + kg) * 128 + row % 128) * 10 + d
-                tiled[4 * dst:4 * dst + 4] = words[f, kg, d]
-    tr = 128 * rs
-    for e in range(experts):
-        for rt in range((rows + tr - 1) // tr):
-            for slab in range(4):
-                for q in range(5 * rs):
-                    for lane in range(64):
-                        i = 64 * q + lane
-                        rl = i // 10
-                        crow, coff = slab * 32 * rs + rl, 4 * (i - rl * 10)
-                        row = rt * tr + crow
-                        if row >= rows:
-                            continue
-                        tpart = (crow >> 7) * 128 * row_bytes + (crow & 127) * ab + coff
-                        for kg in range(G):
-                            t_off = e * rows_pad * row_bytes + rt * tr * row_bytes + tpart + kg * 128 * ab
-                            r_off = (e * rows + row) * row_bytes + coff + kg * ab
-                            assert np.array_equal(tiled[t_off:t_off + 4], packed[r_off:r_off + 4]), (e, rt, crow, kg)
+                dst = ((tile * G + k) * 128 + rr % 128) * 10 + d
+                tiled[4 * dst:4 * dst + 4] = words[f, k, d]
+    assert t_off.min() >= 0 and t_off.max() + 4 <= tiled.size
+    valid = row < rows
+    r_off = (e * rows + row) * row_bytes + coff + kg * 40
+    for b in range(4):
+        assert np.array_equal(tiled[t_off[valid] + b], packed[r_off[valid] + b])
+        assert (tiled[t_off[~valid] + b] == -1).all()
+
+
+@pytest.mark.parametrize("rows", [16400, 16384 + 128, 16384 + 129, 4100, 300])
+def test_tile_major_two_slab_copies_stay_in_bounds(rows):
+    """Dense two-slab launches (256-row tiles) of single-expert 5-bit matrices: every byte
+    a copy reads lies inside the tile-major copy, for rows % 256 in 1..128 (where 128-row
+    padding would leave the last tile's upper slabs outside it) and above."""
+    G = 8
+    t_off, _, _, _, _, rows_pad = _tile_major_offsets(rows, 2, 1, G)
+    tiled_bytes = rows_pad * 40 * G
+    assert t_off.min() >= 0 and t_off.max() + 4 <= tiled_bytes

@@ -64,10 +64,13 @@ void dih_quant_residency_prepare(void *context);
 /* ---- matrices -------------------------------------------------------------------- */
 
 /* Replaces di_quant_matrix_create (quantized.mm:294-315). Checks 1<=experts<=256,
- * rows>=1, columns a multiple of 64 (at most 8192), bits 5 or 8, group 64. A 5-bit matrix
- * with columns a multiple of 512 also holds a second device copy of its codes in 128-row
- * tile-major order (the prefill GEMM reads that one), which every write path below keeps
- * current; its bytes count in dih_quant_residency_bytes. */
+ * rows>=1, columns a multiple of 64, bits 5 or 8, group 64. Unlike the reference, columns
+ * are limited to 8192 (the GEMV kernels hold a call's activations, up to 8192 of them, in
+ * LDS or registers; the model's widest input is 4096): wider matrices are refused here,
+ * with the usual error, rather than by the calls. A 5-bit matrix with columns a multiple of
+ * 512 also holds a second device copy of its codes in 128-row tile-major order, rows padded
+ * to whole 256-row tiles (the prefill GEMM reads that one), which every write path below
+ * keeps current; its bytes count in dih_quant_residency_bytes. */
 void *dih_quant_matrix_create(void *context, int experts, int rows, int columns, int bits,
                               int group, char *error, int capacity);
 /* Replaces di_quant_matrix_buffer (quantized.mm:316-319). index 0 packed, 1 scales,
@@ -90,7 +93,10 @@ int dih_quant_matrix_write(void *matrix, int index, size_t offset, const void *s
 int dih_quant_matrix_commit(void *matrix, char *error, int capacity);
 /* New: device pointer of buffer `index` (0 packed, 1 scales, 2 biases) for callers
  * that fill weights on the device; uploads a dirty staging copy first. Codes of a 5-bit
- * matrix written through it reach the prefill GEMM after dih_quant_matrix_commit. */
+ * matrix written through it are seen by every later call: once the codes' pointer has been
+ * handed out, each call that uses the matrix first rewrites the prefill GEMM's tile-major
+ * copy of the codes (host-synchronous, a pass over the codes), until
+ * dih_quant_matrix_commit after the last write ends that. */
 void *dih_quant_matrix_device(void *matrix, int index);
 /* New: shape query; any out pointer may be NULL. */
 int dih_quant_matrix_shape(void *matrix, int *experts, int *rows, int *columns, int *bits);

@@ -88,6 +88,8 @@ bool sync_matrix(Matrix *m, char *error, int capacity) {
             if (i == 0 && !matrix_retile(m, 0, (size_t)m->experts * m->rows, error, capacity)) return false;
         }
     }
+    // codes may have changed through the device pointer since it was handed out
+    if (m->tiled_stale && !matrix_retile(m, 0, (size_t)m->experts * m->rows, error, capacity)) return false;
     return true;
 }
 
@@ -356,9 +358,11 @@ __attribute__((visibility("default"))) int dih_quant_matrix_commit(void *matrix,
         set_error(error, capacity, "Invalid matrix");
         return -1;
     }
-    if (!sync_matrix(m, error, capacity)) return -1;
-    // codes written through the device pointer reach the tile-major copy here
-    if (!matrix_retile(m, 0, (size_t)m->experts * m->rows, error, capacity)) return -1;
+    // codes written through the device pointer reach the tile-major copy here, and later
+    // calls stop rewriting it
+    if (!sync_matrix(m, error, capacity) || !matrix_retile(m, 0, (size_t)m->experts * m->rows, error, capacity))
+        return -1;
+    m->tiled_stale = false;
     for (int i = 0; i < 3; i++)
         if (m->host[i]) {
             (void)hipHostFree(m->host[i]);
@@ -372,6 +376,9 @@ __attribute__((visibility("default"))) void *dih_quant_matrix_device(void *matri
     if (!m || index < 0 || index > 2) return nullptr;
     char err[8];
     if (!sync_matrix(m, err, sizeof(err))) return nullptr;
+    // writes through the codes' pointer bypass the tile-major copy: keep it rewritten before
+    // every use until the caller commits
+    if (index == 0 && m->tiled) m->tiled_stale = true;
     return m->dev[index];
 }
 
@@ -857,8 +864,8 @@ static int moe_decode(Context *c, const dih_moe_layer *L, const void *x, const f
         bool ok = launch_moe_decode(a, s, error, capacity);
         if (ok && mo.norm_w) {
             prof_stage("decode_norm");
-            ok = launch_rmsnorm(residual, mo.residual_f32, 1, H, mo.norm_w, mo.eps, mo.normed, mo.normed_f32, s, error,
-                                capacity);
+            ok = launch_rmsnorm(residual, mo.residual_f32, 1, H, mo.norm_w, mo.eps, mo.normed, mo.normed_f32, a.probs, s,
+                                error, capacity);
         }
         prof_stage("kernel");
         return ok ? 0 : -1;
@@ -909,7 +916,7 @@ static int moe_decode(Context *c, const dih_moe_layer *L, const void *x, const f
         return -1;
     prof_mark(c, s, "decode_down_merge");
     if (mo.norm_w) {
-        if (!launch_rmsnorm(residual, mo.residual_f32, 1, H, mo.norm_w, mo.eps, mo.normed, mo.normed_f32, s, error,
+        if (!launch_rmsnorm(residual, mo.residual_f32, 1, H, mo.norm_w, mo.eps, mo.normed, mo.normed_f32, probs, s, error,
                             capacity))
             return -1;
         prof_mark(c, s, "decode_norm");

@@ -415,7 +415,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_experts_kernel(DecodeParam
         for (int s = 0; s < 8; s++) total += __expf(__uint_as_float(lane_value(__float_as_uint(sv), s)) - v0);
         if (lane < 8) {
             P.ids[lane] = bad ? 0u : sid;
-            P.probs[lane] = __expf(sv - v0) / total;
+            // NaN marks the step as failed: K3 leaves the residual unchanged
+            P.probs[lane] = bad ? __builtin_nanf("") : __expf(sv - v0) / total;
         }
         if (lane == 0 && bad && P.status) *P.status = 1u;
     }
@@ -505,7 +506,9 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
         float y = sh * sigmoidf_(route);
 #pragma unroll
         for (int s = 0; s < 8; s++) y += part[s][lane] * pr[s];
-        residual_store(P.residual, P.residual_f32, h, (P.residual_f32 ? __uint_as_float(rbits) : bf16_to_f32(rbits)) + y);
+        // NaN probabilities: non-finite router logits, the residual stays as it was
+        if (!__builtin_isnan(pr[0]))
+            residual_store(P.residual, P.residual_f32, h, (P.residual_f32 ? __uint_as_float(rbits) : bf16_to_f32(rbits)) + y);
         if (P.route_out) {
 #pragma unroll
             for (int s = 0; s < 8; s++) P.route_out[(size_t)s * P.H + h] = part[s][lane];

@@ -202,7 +202,8 @@ DIH_DEV uint32_t wave_min_u32(uint32_t v) {
 // Top-8 of up to 256 logits by one wave (graph_top8 gpu_graph.mm:134-146 semantics:
 // repeated wave max, ties to the lowest id; softmax over the chosen eight with the first
 // (largest) subtracted, summed in slot order). Every lane receives ids/probs. `bad` is
-// set when a logit is not finite (the ids are then 0..7 order-free zeros: all 0).
+// set when a logit is not finite: the ids are then all 0 and the probabilities NaN, which
+// the merge kernels take as "leave this token's residual unchanged".
 DIH_DEV void wave_top8(const float *logits, int experts, uint32_t (&ids)[8], float (&probs)[8],
                        bool &bad) {
     const int lane = threadIdx.x & 63;
@@ -236,7 +237,7 @@ DIH_DEV void wave_top8(const float *logits, int experts, uint32_t (&ids)[8], flo
 #pragma unroll
     for (int i = 0; i < 8; i++) { probs[i] = __expf(chosen[i] - chosen[0]); total += probs[i]; }
 #pragma unroll
-    for (int i = 0; i < 8; i++) probs[i] = probs[i] / total;
+    for (int i = 0; i < 8; i++) probs[i] = bad ? __builtin_nanf("") : probs[i] / total;
 }
 
 DIH_DEV float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
@@ -315,3 +316,4 @@ DIH_DEV int xcd_item(int b, int items) {
     const int L = (b & 7) * per + (b >> 3);
     return (b >> 3) < per && L < items ? L : -1;
 }
+

@@ -31,6 +31,9 @@ struct Matrix {
     // apart). Kept equal to dev[0] by every write path (matrix_retile).
     void *tiled = nullptr;
     size_t tiled_bytes = 0;
+    // the codes' device pointer has been handed out since the last dih_quant_matrix_commit:
+    // every call that uses the matrix rewrites the tile-major copy first (sync_matrix)
+    bool tiled_stale = false;
     uint32_t magic = 0x44494d58u;
 
     const uint32_t *packed() const { return static_cast<const uint32_t *>(dev[0]); }
@@ -155,9 +158,11 @@ bool launch_moe_down_merge(const Matrix *down, const float *act, const uint32_t 
                            char *error, int capacity);
 
 // normed[t] = r[t] * rsqrt(mean(r[t]^2) + eps) * w, one block per token (the norm half of
-// graph_merge_norm / prefill_add_norm, gpu_graph.mm:40-61).
+// graph_merge_norm / prefill_add_norm, gpu_graph.mm:40-61). With `probs` (the tokens' top-8
+// probabilities), a token whose probabilities are NaN (non-finite router logits, merge
+// skipped) keeps its normed row.
 bool launch_rmsnorm(const void *r, int r_f32, int tokens, int hidden, const float *w, float eps,
-                    void *out, int out_f32, hipStream_t s, char *error, int capacity);
+                    void *out, int out_f32, const float *probs, hipStream_t s, char *error, int capacity);
 
 bool launch_top8(const void *logits, int logits_bf16, int tokens, int experts, uint32_t *ids,
                  float *probs, uint32_t *status, float *logits_copy, uint32_t *zero_word,
@@ -208,7 +213,8 @@ bool decode_fast_path_ok(const Matrix *router, const Matrix *gate, const Matrix 
                          const Matrix *sd, const Matrix *sr);
 bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int capacity);
 
-constexpr int kArgmaxPer = 4096;   // values per first-level argmax block (partials per call)
+constexpr int kArgmaxPer = 1024;   // values per first-level argmax block (partials per call)
+
 bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
                    uint32_t *next, hipStream_t s, char *error, int capacity);
 

@@ -9,7 +9,9 @@ namespace dih {
 // One wave per token (prefill_top8 gpu_prefill.mm:151-161 / SelectExperts
 // Qwen36Model.cs:246-262): eight rounds of wave max with ties to the lowest expert id,
 // then softmax over the eight chosen logits (largest subtracted, summed in slot order).
-// A non-finite logit sets *status = 1 and the token's ids to 0.
+// A non-finite logit sets *status = 1, the token's ids to 0 and its probabilities to NaN: the
+// merge then leaves that token's residual (and normed row) unchanged, where the reference's
+// host path throws before writing (SelectExperts, Qwen36Model.cs:252).
 __global__ __launch_bounds__(256) void top8_kernel(const void *logits, int logits_bf16, int tokens,
                                                    int experts, uint32_t *ids, float *probs,
                                                    uint32_t *status, float *logits_copy,
@@ -58,7 +60,7 @@ __global__ __launch_bounds__(256) void top8_kernel(const void *logits, int logit
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             ids[(size_t)t * 8 + i] = any_bad ? 0u : picked[i];
-            probs[(size_t)t * 8 + i] = p[i] / total;
+            probs[(size_t)t * 8 + i] = any_bad ? __builtin_nanf("") : p[i] / total;
         }
         if (any_bad && status) *status = 1u;
     }
@@ -179,6 +181,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint32_t *sr_packed,
     float p[8];
 #pragma unroll
     for (int s = 0; s < 8; s++) p[s] = probs[(size_t)t * 8 + s];
+    // a token whose router logits were not finite (NaN probabilities) keeps its residual
+    // and normed row unchanged (uniform over the block: one token)
+    if (__builtin_isnan(p[0])) return;
     const float *sh = route_out + ((size_t)tokens * 8 + t) * H;
     const float *ro = route_out + (size_t)t * 8 * H;
     float ss = 0.f;
@@ -222,9 +227,11 @@ bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens,
 // One block per token: normed[t] = r[t] * rsqrt(sum(r[t]^2)/H + eps) * w (the norm of
 // graph_merge_norm / prefill_add_norm, gpu_graph.mm:40-61).
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *r, int r_f32, int H, const float *w,
-                                                      float eps, void *out, int out_f32) {
+                                                      float eps, void *out, int out_f32, const float *probs) {
     __shared__ float sq[4];
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the token's merge was skipped (non-finite router logits): its normed row stays as it was
+    if (probs && __builtin_isnan(probs[(size_t)t * 8])) return;
     float ss = 0.f;
     for (int c = tid; c < H; c += 256) {
         const float v = residual_load(r, r_f32, (size_t)t * H + c);
@@ -243,16 +250,18 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void *r, int r_f32, 
 }
 
 bool launch_rmsnorm(const void *r, int r_f32, int tokens, int hidden, const float *w, float eps,
-                    void *out, int out_f32, hipStream_t s, char *error, int capacity) {
-    DIH_LAUNCH(rmsnorm_kernel, dim3(tokens), dim3(256), 0, s, r, r_f32, hidden, w, eps, out, out_f32);
+                    void *out, int out_f32, const float *probs, hipStream_t s, char *error, int capacity) {
+    DIH_LAUNCH(rmsnorm_kernel, dim3(tokens), dim3(256), 0, s, r, r_f32, hidden, w, eps, out, out_f32, probs);
     return hip_ok(hipGetLastError(), error, capacity, "norm launch");
 }
 
 // --------------------------------------------------------------------------- argmax
 
 // Two levels, two launches (graph_argmax_blocks/final gpu_graph.mm:160-175): each block of
-// the first reduces 4096 values to (max, lowest index), flagging non-finite values; one block
-// of the second reduces the partials. Result 0xffffffff when any value is not finite. (One
+// the first reduces 1024 values to (max, lowest index), flagging non-finite values (one
+// 16-byte load a thread, so the pass is one memory round trip over 243 blocks for the
+// 248,320 logits; 4096 values a block, 61 blocks, took 5.6 us); one block of the second
+// reduces the partials. Result 0xffffffff when any value is not finite. (One
 // launch with a last-block ticket measured 10.7-12 us: the ticket's release fence and
 // device-scope atomic from every block cost more than the second launch.)
 
@@ -284,18 +293,15 @@ __global__ __launch_bounds__(256) void argmax_blocks_kernel(const float *v, int 
     __shared__ uint32_t wi[4];
     const int tid = threadIdx.x;
     const int base = blockIdx.x * kArgmaxPer;
-    float x[16];
-    // four coalesced 16-byte loads a thread when the block is whole and aligned, else scalar
+    float x[4];
+    // a coalesced 16-byte load a thread when the block is whole and aligned, else scalar
     if (base + kArgmaxPer <= n && (reinterpret_cast<uintptr_t>(v) & 15) == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float4 q = *reinterpret_cast<const float4 *>(v + base + 1024 * k + 4 * tid);
-            x[4 * k] = q.x; x[4 * k + 1] = q.y; x[4 * k + 2] = q.z; x[4 * k + 3] = q.w;
-        }
+        const float4 q = *reinterpret_cast<const float4 *>(v + base + 4 * tid);
+        x[0] = q.x; x[1] = q.y; x[2] = q.z; x[3] = q.w;
     } else {
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int at = base + 1024 * (k >> 2) + 4 * tid + (k & 3);
+        for (int k = 0; k < 4; k++) {
+            const int at = base + 4 * tid + k;
             x[k] = at < n ? v[at] : -INFINITY;
         }
     }
@@ -303,8 +309,8 @@ __global__ __launch_bounds__(256) void argmax_blocks_kernel(const float *v, int 
     uint32_t id = 0xffffffffu;
     bool bad = false;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const int at = base + 1024 * (k >> 2) + 4 * tid + (k & 3);
+    for (int k = 0; k < 4; k++) {
+        const int at = base + 4 * tid + k;
         if (at < n) {
             if (!isfinite(x[k])) bad = true;
             else if (x[k] > best || (x[k] == best && (uint32_t)at < id)) { best = x[k]; id = (uint32_t)at; }
@@ -337,7 +343,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pval, co
 
 bool launch_argmax(const float *values, int n, float *part_val, uint32_t *part_idx,
                    uint32_t *next, hipStream_t s, char *error, int capacity) {
-    static_assert(kArgmaxPer == 16 * 256, "16 values a thread");
+    static_assert(kArgmaxPer == 4 * 256, "4 values a thread");
     const int blocks = (n + kArgmaxPer - 1) / kArgmaxPer;
     DIH_LAUNCH(argmax_blocks_kernel, dim3(blocks), dim3(256), 0, s, values, n, part_val, part_idx);
     if (!hip_ok(hipGetLastError(), error, capacity, "argmax launch")) return false;

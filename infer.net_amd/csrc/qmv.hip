@@ -551,7 +551,9 @@ __global__ __launch_bounds__(512) void moe_down_merge_kernel(
             float y = sh * sigmoidf_(sroute[0]);
 #pragma unroll
             for (int q = 0; q < 8; q++) y += part[q][r] * probs[q];
-            residual_store(residual, residual_f32, h, residual_load(residual, residual_f32, h) + y);
+            // NaN probabilities: non-finite router logits, the residual stays as it was
+            if (!__builtin_isnan(probs[0]))
+                residual_store(residual, residual_f32, h, residual_load(residual, residual_f32, h) + y);
             if (route_out) {
 #pragma unroll
                 for (int q = 0; q < 8; q++) route_out[(size_t)q * H + h] = part[q][r];

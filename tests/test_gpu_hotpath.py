@@ -291,6 +291,46 @@ def test_lm_head_split_logits_and_argmax(device):
             s.dispose()
 
 
+@pytest.mark.parametrize("columns", [2048, 1024])   # the one-shot GEMV, and the general one
+def test_lm_head_argmax_ties_and_nonfinite(device, columns):
+    """The lm_head's token (graph_argmax_blocks/final, gpu_graph.mm:160-175): exact ties
+    between logits in different slices and blocks go to the lowest vocabulary index, and a
+    non-finite logit makes the token invalid (0xffffffff, ModelTests.cs:23-28)."""
+    rng = np.random.default_rng(8)
+    rows = 5000
+    hosts = [orc.random_matrix(rng, 1, rows, columns, 8) for _ in range(4)]
+    # one row with large codes and scales, copied to slice 3 row 4321, slice 1 row 17 and
+    # slice 1 row 4999 (the largest logits, exactly equal): the answer is 1 * rows + 17
+    wpr = columns // 4
+    gpr = columns // 64
+    hot_p = np.full(wpr, 0xFFFFFFFF, dtype=np.uint32)
+    hot_s = np.full(gpr, orc.f32_to_bf16_bits(np.float32(0.5)), dtype=np.uint16)
+    hot_b = np.zeros(gpr, dtype=np.uint16)
+    for k, r in ((3, 4321), (1, 17), (1, 4999)):
+        hosts[k].packed.reshape(rows, wpr)[r] = hot_p
+        hosts[k].scales.reshape(rows, gpr)[r] = hot_s
+        hosts[k].biases.reshape(rows, gpr)[r] = hot_b
+    slices = [upload(device, h) for h in hosts]
+    try:
+        xb = orc.f32_to_bf16_bits(np.abs(rng.normal(size=columns)).astype(np.float32) + 0.5)
+        logits = torch.zeros(4 * rows, dtype=torch.float32, device="cuda")
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        dh.lm_head(device, slices, dev_bf16(xb), logits, nxt)
+        torch.cuda.synchronize()
+        got = logits.cpu().numpy()
+        assert got[rows + 17] == got[rows + 4999] == got[3 * rows + 4321] == got.max()
+        assert int(u32(nxt)[0]) == rows + 17 == orc.argmax(got)
+        # a non-finite activation: every logit NaN, the token invalid
+        xn = xb.copy()
+        xn[5] = orc.f32_to_bf16_bits(np.array([np.inf], dtype=np.float32))[0]
+        dh.lm_head(device, slices, dev_bf16(xn), logits, nxt)
+        torch.cuda.synchronize()
+        assert int(u32(nxt)[0]) == 0xFFFFFFFF
+    finally:
+        for m in slices:
+            m.dispose()
+
+
 def test_argmax_known_answers(device):
     """graph_checks.mm:89-103 and ModelTests.cs:23-28."""
     n = 248320
@@ -311,9 +351,13 @@ def test_argmax_known_answers(device):
 
 
 def test_argmax_block_edges(device):
-    """Ties across the 4096-value first-level blocks, a maximum in a partial last block,
-    and values that start off 16-byte alignment (the scalar load path)."""
+    """Ties across the 1024-value first-level blocks (and at 4096-value boundaries), a
+    maximum in a partial last block, and values that start off 16-byte alignment (the scalar
+    load path)."""
     cases = []
+    t = np.full(3073, -3, dtype=np.float32); t[1023] = t[1024] = t[2048] = 2; cases.append((t, 1023, 0))
+    t = np.full(3073, -3, dtype=np.float32); t[3072] = 5; cases.append((t, 3072, 0))
+    t = np.full(3000, -3, dtype=np.float32); t[2047] = 9; t[5] = np.inf; cases.append((t, 0xFFFFFFFF, 0))
     t = np.full(12289, -3, dtype=np.float32); t[4095] = t[4096] = 2; cases.append((t, 4095, 0))
     t = np.full(12289, -3, dtype=np.float32); t[12288] = 5; cases.append((t, 12288, 0))
     t = np.full(12289, -3, dtype=np.float32); t[8191] = t[8192] = t[12000] = 4; cases.append((t, 8191, 0))
@@ -482,16 +526,19 @@ def test_moe_decode_routing_ties_and_expert_counts(device, E):
         got_lg = lgt.cpu().numpy()
         assert orc.rel_err(got_lg, orc.qmv_f64(L.router, orc.bf16_bits_to_f32(xb))) < 1e-5
         assert np.array_equal(ids.cpu().numpy(), orc.top8(got_lg)[0])
-        # a NaN logit: status 1 and ids 0
+        # a NaN logit: status 1, ids 0, and the residual unchanged
         lg = rng.normal(size=E).astype(np.float32)
         lg[E // 2] = np.nan
         ids = torch.full((8,), 7, dtype=torch.int32, device="cuda")
         status = torch.zeros(1, dtype=torch.int32, device="cuda")
-        dh.moe_decode(device, layer_s, dev_bf16(xb), torch.zeros(H, dtype=torch.int16, device="cuda"),
+        r0 = orc.f32_to_bf16_bits(rng.normal(size=H).astype(np.float32))
+        res = dev_bf16(r0)
+        dh.moe_decode(device, layer_s, dev_bf16(xb), res,
                       logits=torch.from_numpy(lg).cuda(), trace=dh.make_trace(ids=ids, status=status))
         torch.cuda.synchronize()
         assert int(status.item()) == 1
         assert not ids.cpu().numpy().any()
+        assert np.array_equal(res.cpu().numpy().view(np.uint16), r0)
     finally:
         for m in q:
             if m is not None:
@@ -642,12 +689,13 @@ def _device_copy(dst: int, src: int, n: int) -> None:
     assert hip.hipMemcpy(dst, src, n, 4) == 0  # hipMemcpyDefault
 
 
-@pytest.mark.parametrize("path", ["chunks", "staging", "device_ptr"])
+@pytest.mark.parametrize("path", ["chunks", "staging", "device_ptr", "device_ptr_uncommitted"])
 def test_5bit_tile_major_copy_follows_every_write_path(device, path):
     """5-bit matrices with K a multiple of 512 feed the streaming GEMM from a tile-major copy
     of their codes, which every write path must keep equal to the row-major codes: direct
     writes in ragged chunks that start and end inside rows, the host staging buffer, and the
-    device pointer followed by dih_quant_matrix_commit. 200 rows (the copy pads to 256).
+    device pointer followed by dih_quant_matrix_commit, and the device pointer asked for once
+    and written twice without a commit. 200 rows (the copy pads to 256).
     Rows rewritten after a multiply must reach the next multiply."""
     L = dh.load()
     rng = np.random.default_rng(5)
@@ -660,6 +708,7 @@ def test_5bit_tile_major_copy_follows_every_write_path(device, path):
     mixed[37:150] = second.packed.reshape(rows, words)[37:150]
     want_host = orc.QMatrix(mixed, first.scales, first.biases, 1, rows, columns, 5)
     m = device.allocate(1, rows, columns, 5)
+    held = []
 
     def put(packed: np.ndarray, lo: int, hi: int) -> None:
         raw = np.ascontiguousarray(packed).view(np.uint8).reshape(-1)
@@ -672,9 +721,15 @@ def test_5bit_tile_major_copy_follows_every_write_path(device, path):
         else:
             t = torch.from_numpy(raw[lo:hi].copy()).cuda()
             torch.cuda.synchronize()
-            _device_copy(m.device_ptr(0) + lo, t.data_ptr(), hi - lo)
-            err = ctypes.create_string_buffer(256)
-            assert L.dih_quant_matrix_commit(m.handle, err, 256) == 0, err.value
+            if path == "device_ptr":
+                _device_copy(m.device_ptr(0) + lo, t.data_ptr(), hi - lo)
+                err = ctypes.create_string_buffer(256)
+                assert L.dih_quant_matrix_commit(m.handle, err, 256) == 0, err.value
+            else:
+                # the pointer asked for once and kept, no commit: every call rewrites the copy
+                if not held:
+                    held.append(m.device_ptr(0))
+                _device_copy(held[0] + lo, t.data_ptr(), hi - lo)
 
     try:
         row_bytes = words * 4

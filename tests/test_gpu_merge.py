@@ -137,3 +137,90 @@ def test_merge_options_are_validated(device):
         for m in q:
             if m is not None:
                 m.dispose()
+
+
+@pytest.mark.parametrize("bits,E,H,I", [(8, 256, 2048, 512), (8, 16, 1024, 1536)])   # fast and GEMV-stage paths
+@pytest.mark.parametrize("noalloc", [False, True])
+def test_decode_nonfinite_logit_leaves_outputs_unchanged(device, bits, E, H, I, noalloc):
+    """A non-finite router logit fails the step (status 1, ids 0, probabilities NaN) and leaves
+    the residual and the normed row exactly as they were: the reference's host path throws
+    before writing any output (SelectExperts, Qwen36Model.cs:252)."""
+    if noalloc and I > 1024:
+        pytest.skip("the no-allocation entry takes the fast-path shapes only")
+    rng = np.random.default_rng(90 + I)
+    L = _moe_layer(rng, E, H, I, bits)
+    q, layer = _upload_layer(device, L)
+    layer_s = dh.make_layer(None, *q[1:])
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=H).astype(np.float32))
+        for bad in (np.nan, np.inf, -np.inf):
+            lg = rng.normal(size=E).astype(np.float32)
+            lg[E // 3] = bad
+            r0 = orc.f32_to_bf16_bits(rng.normal(size=H).astype(np.float32))
+            res = dev_bf16(r0)
+            normed = torch.full((H,), 7.0, dtype=torch.float32, device="cuda")
+            ids = torch.full((8,), 5, dtype=torch.int32, device="cuda")
+            probs = torch.zeros(8, dtype=torch.float32, device="cuda")
+            status = torch.zeros(1, dtype=torch.int32, device="cuda")
+            call = dh.moe_decode_noalloc if noalloc else dh.moe_decode
+            call(device, layer_s, dev_bf16(xb), res, logits=torch.from_numpy(lg).cuda(),
+                 trace=dh.make_trace(ids=ids, probs=probs, status=status),
+                 merge=dh.make_merge(False, torch.ones(H, device="cuda"), 1e-6, normed, True))
+            torch.cuda.synchronize()
+            assert int(status.item()) == 1, bad
+            assert not ids.cpu().numpy().any()
+            assert np.isnan(probs.cpu().numpy()).all()
+            assert np.array_equal(res.cpu().numpy().view(np.uint16), r0), bad
+            assert (normed.cpu().numpy() == 7.0).all(), bad
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
+@pytest.mark.parametrize("bits", [8, 5])
+def test_prefill_nonfinite_logit_leaves_its_token_unchanged(device, bits):
+    """Prefill with non-finite router logits in two tokens: status 1; those tokens' ids 0,
+    probabilities NaN, residual and normed rows bit-for-bit unchanged; every other token's
+    residual and normed rows bit-for-bit what the same call gives without the bad tokens'
+    logits (their routes then change only their own rows)."""
+    rng = np.random.default_rng(95 + bits)
+    T, E, H, I = 40, 16, 512, 256
+    L = _moe_layer(rng, E, H, I, bits, router=False)
+    q, layer = _upload_layer(device, L)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+        lg = rng.normal(size=(T, E)).astype(np.float32)
+        r0 = orc.f32_to_bf16_bits(rng.normal(size=(T, H)).astype(np.float32))
+        w = torch.from_numpy(rng.uniform(0.5, 1.5, size=H).astype(np.float32)).cuda()
+
+        def run(logits):
+            res = dev_bf16(r0)
+            normed = torch.full((T, H), 3.0, dtype=torch.float32, device="cuda")
+            ids = torch.full((T, 8), 9, dtype=torch.int32, device="cuda")
+            probs = torch.zeros((T, 8), dtype=torch.float32, device="cuda")
+            status = torch.zeros(1, dtype=torch.int32, device="cuda")
+            dh.moe_prefill(device, layer, T, dev_bf16(xb), torch.from_numpy(logits).cuda(), res, logits_dtype=dh.F32,
+                           trace=dh.make_trace(ids=ids, probs=probs, status=status),
+                           merge=dh.make_merge(False, w, 1e-6, normed, True))
+            torch.cuda.synchronize()
+            return (res.cpu().numpy().view(np.uint16), normed.cpu().numpy(), ids.cpu().numpy(), probs.cpu().numpy(),
+                    int(status.item()))
+
+        clean = run(lg)
+        assert clean[4] == 0
+        bad_lg = lg.copy()
+        bad_lg[7, 3] = np.nan
+        bad_lg[30, 0] = np.inf
+        res, normed, ids, probs, status = run(bad_lg)
+        assert status == 1
+        good = np.ones(T, dtype=bool)
+        good[[7, 30]] = False
+        assert not ids[~good].any() and np.isnan(probs[~good]).all()
+        assert np.array_equal(res[~good], r0[~good]) and (normed[~good] == 3.0).all()
+        assert np.array_equal(ids[good], clean[2][good])
+        assert np.array_equal(res[good], clean[0][good]) and np.array_equal(normed[good], clean[1][good])
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()

@@ -61,6 +61,20 @@ def traffic_from_profiles(kernel):
     return None
 
 
+def rocprof_avg_us_from_profiles(kernel):
+    """Average duration (us) of `kernel` from the committed rocprofv3 --kernel-trace summaries
+    (a line `rocprof_avg_us[<kernel>]: <us>` in profiles/*.md), else None."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*rocprof_avg_us\[([^\]]+)\]:\s*([0-9.eE+]+)", line)
+                if m and m.group(1) == kernel:
+                    return float(m.group(2))
+    return None
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -179,6 +193,79 @@ class Bench:
         self.free(built)
         return {"ms_per_step": ms, "bytes_per_step": step_bytes, "GB_s": step_bytes / (ms * 1e-3) / 1e9,
                 "stages": stages}
+
+    def decode_timeline(self, steps, layers=24):
+        """Config 2 decode step with the decode kernels' in-kernel clock stamps (library built
+        with `make timeline`): `steps` steps over `layers` rotating layer copies are captured in
+        one HIP graph and replayed; the stamps hold the last step. Per kernel and stamp point the
+        percentiles over all stamped waves, in us from the first wave entry of that step's router
+        kernel; launch gaps = next kernel's first wave entry - previous kernel's last wave end."""
+        import ctypes
+        import numpy as np
+        torch, dh = self.torch, self.dh
+        L = dh.load()
+        L.dih_decode_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        khz = L.dih_decode_timeline_clock_khz()
+        if khz <= 0:
+            raise RuntimeError("wall clock rate unavailable")
+        built = [self.moe_layer(8) for _ in range(layers)]
+        xs = self.bf16(64, H)
+        res = self.bf16(H)
+        dh.moe_decode(self.dev, built[0][1], xs[0], res)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(steps):
+                    dh.moe_decode(self.dev, built[i % layers][1], xs[i % 64], res)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        reps = []
+        nb, nw, npnt = 512, 16, 4
+        for _ in range(3):
+            if L.dih_decode_timeline_clear() != 0:
+                raise RuntimeError("timeline clear failed")
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            g.replay()
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e3 / steps
+            buf = np.zeros(3 * nb * nw * npnt, dtype=np.uint64)
+            if L.dih_decode_timeline_read(buf.ctypes.data, buf.size) != 0:
+                raise RuntimeError("timeline read failed")
+            reps.append((buf.reshape(3, nb * nw, npnt).astype(np.int64), wall))
+        del g
+        self.free(built)
+        us = 1e3 / khz
+        names = ["decode_router_shared", "decode_experts_gate_up", "decode_down_merge"]
+        points = [["entry", "x staged", "weights arrived + dot", "end"],
+                  ["entry", "ranked, weights requested", "weights arrived + dot", "end"],
+                  ["entry", "weights requested", "weights arrived + dot", "end"]]
+        out = {"clock_khz": khz, "steps": steps, "layers": layers, "replays": []}
+        for T, wall in reps:
+            start = T[0][T[0][:, 0] > 0][:, 0].min()
+            rep = {"graph_us_per_step": wall * 1e3, "kernels": {}}
+            bounds = []
+            for k, name in enumerate(names):
+                t = T[k][(T[k][:, 0] > 0) & (T[k][:, 3] > 0)]
+                kd = {"waves": int(len(t))}
+                for j, pn in enumerate(points[k]):
+                    col = t[:, j][t[:, j] > 0]
+                    v = np.sort((col - start) * us)
+                    kd[pn] = {"p10": round(float(v[len(v) // 10]), 2), "p50": round(float(v[len(v) // 2]), 2),
+                              "p90": round(float(v[int(len(v) * 0.9)]), 2), "max": round(float(v[-1]), 2),
+                              "min": round(float(v[0]), 2)}
+                rep["kernels"][name] = kd
+                bounds.append(((t[:, 0].min() - start) * us, (t[:, 3].max() - start) * us))
+            rep["launch_gaps_us"] = {f"{names[k]} -> {names[k + 1]}": round(float(bounds[k + 1][0] - bounds[k][1]), 2)
+                                     for k in range(2)}
+            rep["step_us_first_entry_to_last_end"] = round(float(bounds[2][1] - bounds[0][0]), 2)
+            out["replays"].append(rep)
+        return out
 
     def qmv(self, steps, warmup, copies=64):
         """Config 1: one 8-bit [4096 x 2048] GEMV, bf16 in/out, rotating 64 weight copies."""
@@ -640,8 +727,16 @@ def main():
         print("bench.py runs as a single process on one GPU.", file=sys.stderr)
         sys.exit(2)
     steps, warmup = max(1, args.steps), max(0, args.warmup)
-    b = Bench(args)
     wls = set(args.workload.split(","))
+    if "decode_timeline" in wls:
+        # the measurement build of the library (make -C infer.net_amd timeline), loaded in
+        # place of the product library before anything else loads it
+        import deepinfer_hip as dh
+        dh.LIB_PATH = os.path.join(os.path.dirname(dh.LIB_PATH), "libdeepinfer_hip_timeline.so")
+        b = Bench(args)
+        print(json.dumps({"decode_timeline": b.decode_timeline(min(steps, 48), layers=args.layers)}), flush=True)
+        return
+    b = Bench(args)
     on = lambda name: "all" in wls or name in wls  # noqa: E731
     res = {}
     if on("decode"):
@@ -704,6 +799,17 @@ def main():
             if "peaks" in res and dom[1]["GB_s"]:
                 roof["measured_peak"] = res["peaks"]["hbm_read_GB_s"]
                 roof["frac_of_measured_peak"] = dom[1]["GB_s"] / res["peaks"]["hbm_read_GB_s"]
+            # every decode kernel's fraction: from this run's HIP events, and from the average
+            # duration the committed rocprofv3 kernel trace of the same command measured
+            kern = {}
+            for name, st in d["stages"].items():
+                rp = rocprof_avg_us_from_profiles(name)
+                kern[name] = {"avg_us": st["avg_us"], "bytes": st["bytes"],
+                              "frac": st["GB_s"] / PEAK_HBM_GBS if st["GB_s"] else None,
+                              "rocprof_avg_us": rp,
+                              "frac_rocprof": st["bytes"] / (rp * 1e3) / PEAK_HBM_GBS if rp and st["bytes"] else None}
+            roof["kernels"] = kern
+            roof["frac_rocprof"] = kern[dom[0]]["frac_rocprof"]
     else:
         k, v = next(iter(res.items()))
         if k == "attention":

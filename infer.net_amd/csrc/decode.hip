@@ -24,6 +24,24 @@
 
 namespace dih {
 
+#ifdef DIH_DECODE_TIMELINE
+// Measurement build only (make timeline): lane 0 of every wave of the first kTlBlocks blocks
+// of each kernel writes the constant 100 MHz clock at four points. Each call overwrites the
+// previous call's stamps, so a read after a sequence holds its last call.
+constexpr int kTlBlocks = 512, kTlWaves = 16, kTlPoints = 4;
+__device__ unsigned long long g_decode_timeline[3 * kTlBlocks * kTlWaves * kTlPoints];
+#define DIH_TL(kern, point)                                                                       \
+    do {                                                                                          \
+        if ((threadIdx.x & 63) == 0 && blockIdx.x < kTlBlocks)                                    \
+            g_decode_timeline[(((kern) * kTlBlocks + blockIdx.x) * kTlWaves + (threadIdx.x >> 6)) * \
+                                  kTlPoints + (point)] = wall_clock64();                          \
+    } while (0)
+#else
+#define DIH_TL(kern, point) \
+    do {                    \
+    } while (0)
+#endif
+
 namespace {
 
 constexpr int kK1Waves = 4;        // waves per K1 block: the launch spreads over many CUs
@@ -267,6 +285,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
     __shared__ float xhs[64], xhm[64];
     const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
+    DIH_TL(0, 0);
     if (b < P.nchunks) {
         // router rows b*chunk + wave*rpw + g (8-bit), one row group a wave
         const int chunk = kK1Waves * kRouterGroups * L.rpw;
@@ -279,11 +298,13 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
             rows_load<8, kRouterGroups>(R, P.rp, P.rs, P.rb, 0, P.E, base, L.rpw, L.g, L.jc, P.H);
             stage_xh_store(xv, P.H, xh, xhs, xhm);
             __syncthreads();
+            DIH_TL(0, 1);
             uint32_t xr[16];
             float mult;
             const float xs = lane_xh(xr, xh, xhs, xhm, L, mult);
             float v[kRouterGroups];
             rows_dot_h8<kRouterGroups>(R, xr, xs, mult, L.valid, L.lpr, v);
+            DIH_TL(0, 2);
 #pragma unroll
             for (int q = 0; q < kRouterGroups; q++) {
                 const int o = wrow + q * L.rpw + L.g;  // row within the block's experts
@@ -292,6 +313,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
         } else if ((int)threadIdx.x < n) {
             P.logits[b * chunk + threadIdx.x] = P.logits_in[b * chunk + threadIdx.x];
         }
+        DIH_TL(0, 3);
         return;
     }
     const int sb = b - P.nchunks;
@@ -306,11 +328,13 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
         if constexpr (BITS == 8) {
             stage_xh_store(xv, P.H, xh, xhs, xhm);
             __syncthreads();
+            DIH_TL(0, 1);
             uint32_t xr[16];
             float mult;
             const float xs = lane_xh(xr, xh, xhs, xhm, L, mult);
             rows_dot_h8<1>(G, xr, xs, mult, L.valid, L.lpr, a);
             rows_dot_h8<1>(U, xr, xs, mult, L.valid, L.lpr, c);
+            DIH_TL(0, 2);
         } else {
             stage_x_store(xv, P.H, xl, xsl);
             __syncthreads();
@@ -320,6 +344,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeParams P) {
             rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, c);
         }
         if (L.j == 0 && base + L.g < P.I) P.sact[base + L.g] = siluf_(a[0]) * c[0];
+        DIH_TL(0, 3);
         return;
     }
     // shared-expert gate row (sigmoid applied at the merge)
@@ -352,6 +377,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_experts_kernel(DecodeParam
     const int slot = blockIdx.x / P.gate_blocks;
     const LaneGeom L = lane_geom(P.H, P.lpr_h);
     const int base = ((blockIdx.x - slot * P.gate_blocks) * kWaves + wave) * L.rpw;
+    DIH_TL(1, 0);
     // The token's experts, ranked once per block in two rounds on 64-bit keys (value desc,
     // id asc, as the reference's insertion with `>`, SelectExperts Qwen36Model.cs:246-261):
     // each group of 32 logits keeps its top-8 (four lanes a logit, eight comparisons each),
@@ -394,6 +420,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_experts_kernel(DecodeParam
     const uint32_t myid = ~(uint32_t)cm[lane];
     const bool bad = any_bad != 0;
     const uint32_t e = bad ? 0u : lane_value(myid, __ffsll((long long)__ballot(myrank == slot)) - 1);
+    DIH_TL(1, 1);
     // one gated row group of expert e per wave
     const size_t ebase = (size_t)e * P.I;
     Rows<BITS, 1> G, U;
@@ -433,7 +460,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_experts_kernel(DecodeParam
         rows_dot<BITS, 1>(G, x, xs, L.valid, L.lpr, a);
         rows_dot<BITS, 1>(U, x, xs, L.valid, L.lpr, u);
     }
+    DIH_TL(1, 2);
     if (L.j == 0 && base + L.g < P.I) P.act[(size_t)slot * P.I + base + L.g] = siluf_(a[0]) * u[0];
+    DIH_TL(1, 3);
 }
 
 // ------------------------------------------------------------------------------- K3
@@ -447,6 +476,7 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int row0 = blockIdx.x * P.down_rows;
     const LaneGeom L = lane_geom(P.I, P.lpr_i);
+    DIH_TL(2, 0);
     // merge operands first (wave 0 lanes < down_rows merge); the residual bits are loaded
     // unconditionally and converted at the merge, so that no wait follows the load
     const int h = row0 + lane;
@@ -477,6 +507,7 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
     const uint16_t *ws = shared ? P.sds : P.ds, *wb = shared ? P.sdb : P.db;
     Rows<BITS, kDownGroups> R;
     rows_load<BITS, kDownGroups>(R, wp, ws, wb, (size_t)e * P.H, P.H, row0, L.rpw, L.g, L.jc, P.I);
+    DIH_TL(2, 1);
     // staging: eight consecutive threads hold the eight float4 of one 32-value chunk
     float *xsums = stage + 9 * P.I;
 #pragma unroll
@@ -497,6 +528,7 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
     const float xs = lane_x_lds(x, stage + wave * P.I, xsums + wave * (P.I >> 5), L);
     float v[kDownGroups];
     rows_dot<BITS, kDownGroups>(R, x, xs, L.valid, L.lpr, v);
+    DIH_TL(2, 2);
 #pragma unroll
     for (int q = 0; q < kDownGroups; q++)
         if (L.j == 0) part[wave][q * L.rpw + L.g] = v[q];
@@ -515,6 +547,7 @@ __global__ __launch_bounds__(576) void decode_down_kernel(DecodeParams P) {
             P.route_out[(size_t)8 * P.H + h] = sh;
         }
     }
+    DIH_TL(2, 3);
 }
 
 // ----------------------------------------------------------------------------- host
@@ -588,3 +621,20 @@ bool launch_moe_decode(const DecodeLaunch &a, hipStream_t s, char *error, int ca
 }
 
 }  // namespace dih
+
+#ifdef DIH_DECODE_TIMELINE
+// Measurement build only: copy out / clear the stamps (layout [kernel][block][wave][point]).
+extern "C" __attribute__((visibility("default"))) int dih_decode_timeline_read(unsigned long long *host, int n) {
+    if (n < 0 || (size_t)n > sizeof(dih::g_decode_timeline) / 8) return -1;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(dih::g_decode_timeline), (size_t)n * 8) == hipSuccess ? 0 : -1;
+}
+extern "C" __attribute__((visibility("default"))) int dih_decode_timeline_clock_khz() {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    return hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess ? khz : -1;
+}
+extern "C" __attribute__((visibility("default"))) int dih_decode_timeline_clear() {
+    static unsigned long long zero[sizeof(dih::g_decode_timeline) / 8];
+    return hipMemcpyToSymbol(HIP_SYMBOL(dih::g_decode_timeline), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#endif

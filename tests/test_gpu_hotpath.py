@@ -326,6 +326,35 @@ def test_lm_head_argmax_ties_and_nonfinite(device, columns):
         dh.lm_head(device, slices, dev_bf16(xn), logits, nxt)
         torch.cuda.synchronize()
         assert int(u32(nxt)[0]) == 0xFFFFFFFF
+        # the next call starts clean (the invalid mark does not carry over)
+        dh.lm_head(device, slices, dev_bf16(xb), logits, nxt)
+        torch.cuda.synchronize()
+        assert int(u32(nxt)[0]) == rows + 17
+    finally:
+        for m in slices:
+            m.dispose()
+
+
+@pytest.mark.parametrize("columns", [2048, 1024])
+def test_lm_head_argmax_all_negative_logits(device, columns):
+    """Every logit negative (biases of -8 against a positive activation): the token is
+    still the largest logit, lowest index first; two calls in a row agree."""
+    rng = np.random.default_rng(9)
+    rows = 3001
+    hosts = [orc.random_matrix(rng, 1, rows, columns, 8) for _ in range(3)]
+    for h in hosts:
+        h.biases[:] = orc.f32_to_bf16_bits(np.float32(-8.0))
+    slices = [upload(device, h) for h in hosts]
+    try:
+        xb = orc.f32_to_bf16_bits(np.abs(rng.normal(size=columns)).astype(np.float32) + 0.5)
+        logits = torch.zeros(3 * rows, dtype=torch.float32, device="cuda")
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        for _ in range(2):
+            dh.lm_head(device, slices, dev_bf16(xb), logits, nxt)
+            torch.cuda.synchronize()
+            got = logits.cpu().numpy()
+            assert got.max() < 0
+            assert int(u32(nxt)[0]) == orc.argmax(got)
     finally:
         for m in slices:
             m.dispose()

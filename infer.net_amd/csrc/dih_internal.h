@@ -56,6 +56,9 @@ struct Context {
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t start = nullptr, stop = nullptr;
+    // side stream of the prefill MoE step (the shared expert beside the routed experts)
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     bool resident = false;
     uint64_t weight_bytes = 0;
     // profiling: one start/stop event pair per kernel launch of device-resident calls,
@@ -186,6 +189,9 @@ struct QmmArgs {
     void *y = nullptr; int y_bf16 = 0;  // output rows indexed by route
 };
 bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity);
+// The grouped gate/up launch of `tokens` tokens over `gate` takes the wide (96/128-route)
+// 5-bit tiles: 5-bit, K a multiple of 512, more than 48 routes an expert on average.
+bool qmm_wide_gated(const Matrix *gate, int tokens);
 
 bool launch_moe_merge(const Matrix *shared_route, const uint16_t *x, int tokens, int hidden,
                       const float *route_out, const float *probs, void *residual,

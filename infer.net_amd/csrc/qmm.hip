@@ -815,6 +815,11 @@ static size_t qmm_max_work(int rows, int tokens, int ngroups, int dense, int bn,
     return row_tiles * (routes / bn + std::min<size_t>((size_t)ngroups, routes));
 }
 
+bool qmm_wide_gated(const Matrix *gate, int tokens) {
+    return gate->bits == 5 && gate->columns % 512 == 0 &&
+           (size_t)tokens * 8 > (size_t)48 * (size_t)std::max(1, gate->experts);
+}
+
 bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     QmmParams P{};
     const Matrix *m0 = a.m0, *m1 = a.m1;
@@ -854,8 +859,7 @@ bool launch_qmm(const QmmArgs &a, hipStream_t s, char *error, int capacity) {
     // more than 48 routes (uniform routing over E experts: 8T/E): 64-route tiles would give
     // an expert of 65-127 routes a second, mostly empty chunk and dequantize its weights
     // twice (config 4: 64 routes on average, at most ~90)
-    const bool wide_gated = streaming && gated && !a.dense && m0->bits == 5 &&
-                            (size_t)a.tokens * 8 > (size_t)48 * (size_t)std::max(1, m0->experts);
+    const bool wide_gated = streaming && gated && !a.dense && qmm_wide_gated(m0, a.tokens);
     // The grouped 5-bit down projection takes 96-route tiles (still two blocks a CU) when
     // experts average more than 48 routes: config 4's experts (at most ~90 routes) then need
     // one chunk each (down 126 -> 119 us; 128-route tiles, one block a CU, measured 211 ->

@@ -635,6 +635,45 @@ def test_moe_prefill_matches_oracle(device, T, E, H, I, bits, routing):
                 m.dispose()
 
 
+def test_moe_prefill_side_stream_graph_replays(device):
+    """Wide 5-bit routing runs the shared expert's launches on the library's side stream
+    (fork and join through events). Captured in a HIP graph with that fork, every replay,
+    with eager work between them, must give the eager call's residual bit for bit."""
+    T, E, H, I = 200, 16, 512, 256
+    rng = np.random.default_rng(31)
+    L = _moe_layer(rng, E, H, I, 5, router=False)
+    q, layer = _upload_layer(device, L)
+    try:
+        x = dev_bf16(orc.f32_to_bf16_bits(rng.normal(size=(T, H)).astype(np.float32)))
+        lg = dev_bf16(orc.f32_to_bf16_bits(rng.normal(size=(T, E)).astype(np.float32)))
+        r0 = dev_bf16(orc.f32_to_bf16_bits(rng.normal(size=(T, H)).astype(np.float32)))
+        want = r0.clone()
+        dh.moe_prefill(device, layer, T, x, lg, want)
+        torch.cuda.synchronize()
+        res = r0.clone()
+        other = r0.clone()
+        g = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                dh.moe_prefill(device, layer, T, x, lg, res)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            res.copy_(r0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(res, want)
+            dh.moe_prefill(device, layer, T, x, lg, other)   # eager work between replays
+            torch.cuda.synchronize()
+        del g
+    finally:
+        for m in q:
+            if m is not None:
+                m.dispose()
+
+
 @pytest.mark.parametrize("bits,rows,columns,T", [(8, 512, 2048, 256), (5, 300, 512, 130), (8, 129, 256, 65),
                                                  (8, 2048, 4096, 64), (8, 1000, 2048, 1), (5, 300, 512, 3),
                                                  (8, 129, 4096, 4), (8, 1003, 2048, 3)])

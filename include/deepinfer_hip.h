@@ -249,7 +249,10 @@ int dih_moe_decode_noalloc(void *context, const dih_moe_layer *layer, const void
  * gate/up + SwiGLU over gathered tokens -> bf16 MFMA down -> weighted sum with the
  * sigmoid-gated shared expert -> residual = bf16(residual + y). x, residual bf16 [T][H].
  * Scratch lives in the context and grows on demand (hipMalloc only when a larger chunk
- * than any before is seen). */
+ * than any before is seen). With 5-bit experts averaging more than 48 routes, the shared
+ * expert's gate/up and down run on the context's side stream, forked from `stream` and
+ * joined back into it through events (both branches land in a graph captured on
+ * `stream`): the call's work is complete when `stream`'s work is. */
 int dih_moe_prefill(void *context, const dih_moe_layer *layer, int tokens, const void *x,
                     const void *logits, int logits_dtype, void *residual,
                     const dih_moe_trace *trace, void *stream, char *error, int capacity);

@@ -223,6 +223,11 @@ __attribute__((visibility("default"))) void *dih_quant_create_configured(int res
         !hip_ok(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking), error, capacity, "stream") ||
         !hip_ok(hipEventCreateWithFlags(&c->fork, hipEventDisableTiming), error, capacity, "event") ||
         !hip_ok(hipEventCreateWithFlags(&c->join, hipEventDisableTiming), error, capacity, "event")) {
+        // release whatever was created before the failure
+        for (hipEvent_t e : {c->start, c->stop, c->fork, c->join})
+            if (e) (void)hipEventDestroy(e);
+        for (hipStream_t st : {c->side, c->stream})
+            if (st) (void)hipStreamDestroy(st);
         delete c;
         return nullptr;
     }

@@ -1030,8 +1030,9 @@ __attribute__((visibility("default"))) int dih_moe_prefill_norm(void *ctx, const
     // Wide 5-bit routing (the routed experts' gate/up work items fill whole rounds of the
     // GPU's one-block-a-CU slots): the shared expert's gate/up and down run as launches of
     // their own on a side stream, so that its items and the routed down projection fill the
-    // tail of the routed gate/up instead of adding a round (config 4: 353-360 -> 339-341 us; 8-bit
-    // Zipf routing measured slower so and keeps one launch for both)
+    // tail of the routed gate/up instead of adding a round (config 4: 353-360 -> 339-341 us
+    // over two graph-replayed steps, 371-372 -> 355-358 us over ten; 8-bit Zipf routing
+    // measured slower so and keeps one launch for both)
     const bool beside = qmm_wide_gated(gate, tokens);
     hipStream_t ss = beside ? c->side : s;
     if (beside && (!hip_ok(hipEventRecord(c->fork, s), error, capacity, "event") ||
@@ -1044,25 +1045,32 @@ __attribute__((visibility("default"))) int dih_moe_prefill_norm(void *ctx, const
     a.y = actb; a.y_bf16 = 1;
     if (beside) a.ngroups = E;
     else { a.sm0 = sg; a.sm1 = su; }
-    if (!launch_qmm(a, s, error, capacity)) return -1;
     QmmArgs as = a;
     as.m0 = sg; as.m1 = su; as.sm0 = as.sm1 = nullptr;
     as.routes = routes + (size_t)E * T; as.counts = counts + E; as.ngroups = 1;
-    if (beside && !launch_qmm(as, ss, error, capacity)) return -1;
-    prof_mark(c, s, "prefill_gate_up");
     QmmArgs d;
     d.m0 = down; d.tokens = tokens; d.routes = routes; d.counts = counts; d.ngroups = E + 1;
     d.x = actb; d.in_mode = 0; d.y = route_out; d.y_bf16 = 0;
     if (beside) d.ngroups = E;
     else d.sm0 = sd;
-    if (!launch_qmm(d, s, error, capacity)) return -1;
     QmmArgs ds = d;
     ds.m0 = sd; ds.sm0 = nullptr;
     ds.routes = routes + (size_t)E * T; ds.counts = counts + E; ds.ngroups = 1;
-    if (beside && (!launch_qmm(ds, ss, error, capacity) ||
-                   !hip_ok(hipEventRecord(c->join, ss), error, capacity, "event") ||
-                   !hip_ok(hipStreamWaitEvent(s, c->join, 0), error, capacity, "event")))
-        return -1;
+    bool ok = launch_qmm(a, s, error, capacity) && (!beside || launch_qmm(as, ss, error, capacity));
+    if (ok) prof_mark(c, s, "prefill_gate_up");
+    ok = ok && launch_qmm(d, s, error, capacity) && (!beside || launch_qmm(ds, ss, error, capacity));
+    // the side stream joins back even after a failed launch, so that a stream under capture
+    // is left with one branch
+    if (beside) {
+        char jerr[256];
+        const bool joined = hip_ok(hipEventRecord(c->join, ss), jerr, sizeof(jerr), "event") &&
+                            hip_ok(hipStreamWaitEvent(s, c->join, 0), jerr, sizeof(jerr), "event");
+        if (ok && !joined) {
+            set_error(error, capacity, jerr);
+            ok = false;
+        }
+    }
+    if (!ok) return -1;
     prof_mark(c, s, "prefill_down");
     if (!launch_moe_merge(sr, static_cast<const uint16_t *>(x), tokens, H, route_out, probs, residual, mo, s,
                           error, capacity))

@@ -717,7 +717,7 @@ def test_dense_long_chunks_bf16_gemm(device, bits, rows, columns, T, y_bf16):
         xb = orc.f32_to_bf16_bits(rng.normal(size=(T, columns)).astype(np.float32))
         y = torch.zeros((T, rows), dtype=torch.int16 if y_bf16 else torch.float32, device="cuda")
         dh.dense(device, m, T, dev_bf16(xb), y, y_dtype=dh.BF16 if y_bf16 else dh.F32)
-        # a second call reuses the cached plan
+        # a second call (the scratch copy already sized) gives the same bits
         y2 = torch.zeros_like(y)
         dh.dense(device, m, T, dev_bf16(xb), y2, y_dtype=dh.BF16 if y_bf16 else dh.F32)
         torch.cuda.synchronize()
@@ -728,6 +728,31 @@ def test_dense_long_chunks_bf16_gemm(device, bits, rows, columns, T, y_bf16):
             assert_rounded(host_bf16(y), want_bf, rms(want_bf) * 1e-2)
         else:
             assert orc.rel_err(y.cpu().numpy(), want_bf) < 1e-4
+    finally:
+        m.dispose()
+
+
+@pytest.mark.parametrize("bits,rows,columns,T,y_bf16", [
+    (8, 8200, 2048, 4100, True),    # 256 x 256 tiles; ragged last row and token tiles
+    (8, 2050, 4096, 4100, False),   # 256 x 128 tiles; f32 rows not 16-byte aligned (element stores)
+    (5, 1000, 1024, 4096, True)])   # 128 x 128 tiles, 5-bit dequantization
+def test_dense_gemm_tile_shapes(device, bits, rows, columns, T, y_bf16):
+    """Every block shape of the library's bf16 GEMM (gemm_bf16_kernel, chosen by the tile
+    count) against the fp64 product of the same bf16-rounded operands, with partial tiles at
+    both edges."""
+    rng = np.random.default_rng(rows + T)
+    host = orc.random_matrix(rng, 1, rows, columns, bits)
+    m = upload(device, host)
+    try:
+        xb = orc.f32_to_bf16_bits(rng.normal(size=(T, columns)).astype(np.float32))
+        y = torch.zeros((T, rows), dtype=torch.int16 if y_bf16 else torch.float32, device="cuda")
+        dh.dense(device, m, T, dev_bf16(xb), y, y_dtype=dh.BF16 if y_bf16 else dh.F32)
+        torch.cuda.synchronize()
+        want = orc.dense_f64_blas(host, orc.bf16_bits_to_f32(xb), round_operands=True)
+        if y_bf16:
+            assert_rounded(host_bf16(y), want, rms(want) * 1e-2)
+        else:
+            assert orc.rel_err(y.cpu().numpy(), want) < 1e-4
     finally:
         m.dispose()
 

@@ -15,10 +15,14 @@ same steps run again directly after the timed replay; `roofline.achieved` is the
 kernel's algorithmic bytes per launch over its average duration. `roofline.traffic` is
 the HBM bytes per launch that rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE measured for that
 kernel, scaled by the counters' reading for a plain copy of known size, read from the
-summaries committed under profiles/ (null when none is present).
+summaries committed under profiles/ (null when none is present). `roofline.kernels` gives
+every decode kernel's fraction from these events and from the rocprofv3 kernel-trace
+average committed under profiles/ (`frac_rocprof`; the dominant kernel's is also
+`roofline.frac_rocprof`).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|qmv|prefill|
-                 prefill5|dense|lm_head|peaks|copycal] [--layers L] [--cpu-seconds S] [--no-cpu]
+                 prefill5|dense|lm_head|peaks|copycal|decode_timeline] [--layers L]
+                [--cpu-seconds S] [--no-cpu]
 """
 import argparse
 import json

@@ -330,6 +330,9 @@ class Bench:
         def stage_ms(name):
             tot, cnt = prof.get(name, (0, 1))
             return tot / max(cnt, 1)
+        # (with the shared expert's launches on the library's side stream, config 4's
+        # gate/up interval covers the routed launch and the down interval the rest up to the
+        # join, so these per-stage rates are approximate there; ms_per_step is not affected)
         gu_ms = stage_ms("prefill_gate_up")
         dn_ms = stage_ms("prefill_down")
         gu_bytes = (touched + 1) * 2 * qbytes(1, I, H, bits)

@@ -47,7 +47,9 @@ typedef struct dih_job {
 /* ---- context ------------------------------------------------------------------- */
 
 /* Replaces di_quant_create (quantized.mm:282-286). Uses device 0 of the process's
- * visible HIP devices and creates one blocking stream (ordered against the null stream). */
+ * visible HIP devices and creates one blocking stream (ordered against the null stream),
+ * plus a non-blocking side stream that dih_moe_prefill forks from and joins back into the
+ * call's stream (default priority, both). */
 void *dih_quant_create(char *error, int capacity);
 /* Replaces di_quant_create_configured (quantized.mm:242-281). `resident` (0/1) and
  * `refresh` (0..60000 ms) are validated like the reference; HIP device memory needs no

@@ -22,8 +22,9 @@
  *     fills on the null stream are complete before a NULL-stream call reads them.
  *   - Entry points named dih_quant_* take HOST pointers and are synchronous, like the
  *     reference's di_quant_* functions.
- *   - A context is single-stream and has no internal locking: callers serialize calls on
- *     one context (the reference serializes through Qwen36Model.cs:18, 47).
+ *   - A call's work is complete when its stream's work is (dih_moe_prefill's side-stream
+ *     branch joins back into it). A context has no internal locking: callers serialize
+ *     calls on one context (the reference serializes through Qwen36Model.cs:18, 47).
  */
 #ifndef DEEPINFER_HIP_H
 #define DEEPINFER_HIP_H
